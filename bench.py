@@ -1,0 +1,205 @@
+"""Benchmark of the MI355X FlashAttention-2 forward (FP16, D=64).
+
+Prints ONE JSON line. The measured workload is the reference's headline
+configuration, B=1 H=8 N=1024 D=64 FP16 (reference README.md:9-42): one step is
+one noncausal forward plus one causal forward through the product entry point
+`flash_attention_cuda.tensorcore_attention_forward_production_128x128`, on
+synthetic inputs already resident in HBM.
+
+Inside the timed region the K steps run as K back-to-back noncausal calls followed
+by K back-to-back causal calls (the same work as K interleaved steps), with HIP
+events on the launch stream at the start, between the two batches and at the
+end - the reference harness's method (benchmarks/harness.py:34-71: events around
+back-to-back calls). Those events give each kernel's average launch duration for
+the `roofline` object; wall-clock time between two device synchronisations gives
+`ms_per_step`.
+
+Also reported (extra keys, each timed the same way after the main region):
+`north_star` - B16 H16 N4096 noncausal and causal (the >=50%-of-MFMA-peak target)
+and B2 H32 N16384 causal with sigma=2 logits; `cpu_baseline` - the oracle's FP32
+CPU restatement of the reference (oracle.attention_reference) timed on this host's
+cores on a bounded sample of the same workload.
+
+FLOPs: 4*B*H*N^2*D per forward, halved for causal. Bytes: 8*B*H*N*D (read Q, K, V
+and write O once, FP16).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+MI355X_FP16_DENSE_TFLOPS = 2516.6  # 256 CUs x 4 SIMDs x 1024 FLOP/clk x 2.4 GHz
+MI355X_HBM_GBPS = 8000.0
+
+# Reference's published medians on an RTX 4070 Laptop GPU (reference README.md:21-42):
+# N=1024 noncausal 65.7 us (runs 65.7/65.4/65.7), causal 53.4 us (53.1/55.4/53.4).
+REFERENCE_US = {"noncausal": 65.7, "causal": 53.4}
+
+METRIC = "fwd attention TFLOP/s + µs, B1 H8 N1024 D64 fp16, causal & noncausal"
+
+
+def attention_flops(batch, heads, seq_len, head_dim, causal):
+    flops = 4.0 * batch * heads * seq_len * seq_len * head_dim
+    return flops / 2 if causal else flops
+
+
+def attention_bytes(batch, heads, seq_len, head_dim):
+    return 8.0 * batch * heads * seq_len * head_dim
+
+
+def make_inputs(batch, heads, seq_len, *, seed=0, sigma=1.0, device="cpu"):
+    import torch
+
+    gen = torch.Generator().manual_seed(seed)
+    shape = (batch, heads, seq_len, 64)
+    q = torch.randn(shape, generator=gen)
+    k = torch.randn(shape, generator=gen)
+    v = torch.randn(shape, generator=gen)
+    return tuple(t.half().to(device) for t in (q * sigma, k * sigma, v))
+
+
+def time_kernel_batches(entry, inputs, modes, steps, warmup):
+    """Runs `warmup` untimed rounds, then for each mode `steps` back-to-back calls
+    between HIP events on the current stream. Returns (wall_s, {mode: avg_s})."""
+    import torch
+
+    q, k, v = inputs
+    for _ in range(warmup):
+        for causal in modes:
+            entry(q, k, v, causal)
+    stream = torch.cuda.current_stream()
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(len(modes) + 1)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    events[0].record(stream)
+    for i, causal in enumerate(modes):
+        for _ in range(steps):
+            entry(q, k, v, causal)
+        events[i + 1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_kernel = {("causal" if causal else "noncausal"): events[i].elapsed_time(events[i + 1]) / 1e3 / steps
+                  for i, causal in enumerate(modes)}
+    return wall, per_kernel
+
+
+def roofline(flops, avg_s):
+    achieved = flops / avg_s / 1e12
+    return {"bound": "mfma", "achieved": round(achieved, 3), "peak": MI355X_FP16_DENSE_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(achieved / MI355X_FP16_DENSE_TFLOPS, 5), "traffic": None}
+
+
+def cpu_baseline(budget_s):
+    """Oracle (FP32 torch restatement of the reference) on this host's CPU cores."""
+    import torch
+
+    from oracle import attention_reference
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    q, k, v = make_inputs(1, 8, 1024)
+    flops = 0.0
+    runs = 0
+    attention_reference(q, k, v, causal=False)  # warmup
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s or runs < 2:
+        for causal in (False, True):
+            attention_reference(q, k, v, causal=causal)
+            flops += attention_flops(1, 8, 1024, 64, causal)
+        runs += 1
+    elapsed = time.perf_counter() - t0
+    return {"value": round(flops / elapsed / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{runs} steps of B1 H8 N1024 D64 (one noncausal + one causal "
+                      f"oracle.attention_reference call each, FP32 CPU), {elapsed:.1f} s",
+            "ms_per_step": round(elapsed / runs * 1e3, 3)}
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=30)
+    parser.add_argument("--north-star-steps", type=int, default=20)
+    parser.add_argument("--cpu-seconds", type=float, default=10.0)
+    parser.add_argument("--skip-north-star", action="store_true")
+    parser.add_argument("--skip-cpu", action="store_true")
+    args = parser.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the attention forward shards over "
+              "batch*heads with no communication, so N>1 is not run here.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import flash_attention_2_lab_amd as fa
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    entry = fa.flash_attention_cuda.tensorcore_attention_forward_production_128x128
+
+    modes = (False, True)
+    inputs = make_inputs(1, 8, 1024, device="cuda")
+    wall, per_kernel = time_kernel_batches(entry, inputs, modes, args.steps, args.warmup)
+    step_flops = sum(attention_flops(1, 8, 1024, 64, c) for c in modes)
+    ms_per_step = wall / args.steps * 1e3
+    value = step_flops / (wall / args.steps) / 1e12
+    ref_step_s = sum(REFERENCE_US.values()) * 1e-6
+    flops_by_mode = {"noncausal": attention_flops(1, 8, 1024, 64, False),
+                     "causal": attention_flops(1, 8, 1024, 64, True)}
+    dominant = max(per_kernel, key=lambda m: per_kernel[m])
+    line = {
+        "metric": METRIC,
+        "value": round(value, 4),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(value / (step_flops / ref_step_s / 1e12), 4),
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "B1 H8 N1024 D64 fp16; one step = one noncausal + one causal forward",
+                   "batch": 1, "heads": 8, "seq_len": 1024, "head_dim": 64,
+                   "baseline_hardware": "RTX 4070 Laptop (reference README.md:21-42)"},
+        "us": {m: round(t * 1e6, 3) for m, t in per_kernel.items()},
+        "roofline": dict(roofline(flops_by_mode[dominant], per_kernel[dominant]), kernel=dominant,
+                         hbm_frac=round(attention_bytes(1, 8, 1024, 64) / per_kernel[dominant]
+                                        / 1e9 / MI355X_HBM_GBPS, 5)),
+    }
+    del inputs
+
+    if not args.skip_north_star:
+        north = {}
+        big = make_inputs(16, 16, 4096, device="cuda")
+        _, t = time_kernel_batches(entry, big, modes, args.north_star_steps, 3)
+        for mode, avg in t.items():
+            f = attention_flops(16, 16, 4096, 64, mode == "causal")
+            north[f"B16H16N4096_{mode}"] = {"us": round(avg * 1e6, 2), "tflops": round(f / avg / 1e12, 2),
+                                            "roofline": roofline(f, avg)}
+        del big
+        long_ctx = make_inputs(2, 32, 16384, sigma=2.0, device="cuda")
+        _, t = time_kernel_batches(entry, long_ctx, (True,), max(3, args.north_star_steps // 4), 1)
+        f = attention_flops(2, 32, 16384, 64, True)
+        north["B2H32N16384_causal_sigma2"] = {"us": round(t["causal"] * 1e6, 2),
+                                              "tflops": round(f / t["causal"] / 1e12, 2),
+                                              "roofline": roofline(f, t["causal"])}
+        del long_ctx
+        line["north_star"] = north
+
+    if not args.skip_cpu:
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,117 @@
+"""In-tree build of the MI355X FlashAttention-2 libraries.
+
+Two shared objects are produced next to this file:
+
+* ``libfa2_mi355x.so`` - the HIP kernels and the C ABI of ``include/fa2_mi355x.h``,
+  compiled by hipcc for gfx950 only.
+* ``flash_attention_cuda<EXT_SUFFIX>`` - the PyTorch operator module with the
+  reference's entry-point names, compiled as host C++ against torch's headers and
+  linked to ``libfa2_mi355x.so`` through an ``$ORIGIN`` rpath.
+
+Both are plain compiler invocations (hipcc cross-compiles gfx950 without a GPU);
+nothing is hipified and no JIT cache is used, so the built files travel with the
+source tree.
+
+Usage: ``python -m flash_attention_2_lab_amd._build``.
+"""
+
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+import sysconfig
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+REPO_ROOT = PACKAGE_DIR.parent
+CSRC = PACKAGE_DIR / "csrc"
+INCLUDE = REPO_ROOT / "include"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+HIPCC = str(ROCM / "bin" / "hipcc")
+
+KERNEL_LIBRARY = PACKAGE_DIR / "libfa2_mi355x.so"
+EXTENSION_NAME = "flash_attention_cuda"
+EXTENSION_LIBRARY = PACKAGE_DIR / (EXTENSION_NAME + sysconfig.get_config_var("EXT_SUFFIX"))
+BUILD_DIR = REPO_ROOT / "_build"
+
+GPU_ARCH = "gfx950"
+
+# Packed FP32 VALU instructions are kept out of generated code (the compiler would
+# otherwise form v_pk_{add,mul,fma}_f32 from scalar float code).
+HIP_FLAGS = [
+    f"--offload-arch={GPU_ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd)}\n{proc.stdout}")
+    # hipcc's host pass warns that it does not know the packed-fp32 target feature.
+    noise = ("packed-fp32-ops", "not a recognized feature")
+    lines = [ln for ln in proc.stdout.splitlines() if ln.strip() and not any(n in ln for n in noise)]
+    if lines:
+        print("\n".join(lines), file=sys.stderr)
+
+
+def kernel_library_command() -> list[str]:
+    return [HIPCC, *HIP_FLAGS, "-shared", f"-I{INCLUDE}",
+            str(CSRC / "fa2_forward.hip"), "-o", str(KERNEL_LIBRARY)]
+
+
+def _extension_flags() -> tuple[list[str], list[str]]:
+    import torch
+    from torch.utils import cpp_extension
+
+    includes = [f"-I{p}" for p in cpp_extension.include_paths()]
+    torch_lib = cpp_extension.library_paths()[0]
+    py_include = sysconfig.get_paths()["include"]
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    compile_flags = [
+        "-O2", "-std=c++17", "-fPIC",
+        "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+        f"-DTORCH_EXTENSION_NAME={EXTENSION_NAME}", "-DTORCH_API_INCLUDE_EXTENSION_H",
+        f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+        *includes, f"-I{py_include}", f"-I{INCLUDE}", f"-I{ROCM / 'include'}",
+    ]
+    link_flags = [
+        f"-L{PACKAGE_DIR}", "-lfa2_mi355x",
+        f"-L{torch_lib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python",
+        "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{torch_lib}",
+    ]
+    return compile_flags, link_flags
+
+
+def extension_commands(object_file: Path) -> tuple[list[str], list[str]]:
+    compile_flags, link_flags = _extension_flags()
+    compile_cmd = ["g++", *compile_flags, "-c", str(CSRC / "flash_attention_cuda.cpp"),
+                   "-o", str(object_file)]
+    link_cmd = ["g++", "-shared", str(object_file), *link_flags, "-o", str(EXTENSION_LIBRARY)]
+    return compile_cmd, link_cmd
+
+
+def build(verbose: bool = False) -> None:
+    """Compile both libraries in place (always recompiles)."""
+    BUILD_DIR.mkdir(exist_ok=True)
+    object_file = BUILD_DIR / "flash_attention_cuda.o"
+    compile_cmd, link_cmd = extension_commands(object_file)
+    # The HIP library and the extension's object file compile in parallel; the
+    # extension links against the HIP library afterwards.
+    with ThreadPoolExecutor(max_workers=2) as pool:
+        jobs = [pool.submit(_run, kernel_library_command()), pool.submit(_run, compile_cmd)]
+        for job in jobs:
+            job.result()
+    _run(link_cmd)
+    if verbose:
+        print(f"built {KERNEL_LIBRARY.name} and {EXTENSION_LIBRARY.name} in {PACKAGE_DIR}")
+
+
+if __name__ == "__main__":
+    build(verbose=True)

@@ -1,0 +1,101 @@
+"""ctypes binding of the C ABI declared in ``include/fa2_mi355x.h``.
+
+This is the binding a Python caller without the torch extension would write; the
+tests use it to exercise the C ABI directly. Tensors are passed as device pointers
+plus sizes, and the kernel is enqueued on the given HIP stream (default: torch's
+current stream on the tensors' device).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import torch
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+LIBRARY_PATH = PACKAGE_DIR / "libfa2_mi355x.so"
+HEADER_PATH = PACKAGE_DIR.parent / "include" / "fa2_mi355x.h"
+
+FA2_STATUS_SUCCESS = 0
+FA2_STATUS_NULL_POINTER = 1
+FA2_STATUS_NEGATIVE_DIMENSION = 2
+FA2_STATUS_BAD_HEAD_DIM = 3
+FA2_STATUS_BAD_SEQUENCE_LENGTH = 4
+FA2_STATUS_MISALIGNED = 5
+FA2_STATUS_TOO_LARGE = 6
+FA2_STATUS_HIP_ERROR_BASE = 1000
+
+
+class Fa2Error(RuntimeError):
+    """A non-zero status from the C ABI."""
+
+    def __init__(self, function: str, status: int, message: str) -> None:
+        super().__init__(f"{function} failed with status {status}: {message}")
+        self.status = status
+
+
+def _load() -> ctypes.CDLL:
+    if not LIBRARY_PATH.exists():
+        raise ImportError(
+            f"{LIBRARY_PATH} is missing (run `python -m flash_attention_2_lab_amd._build`)"
+        )
+    lib = ctypes.CDLL(str(LIBRARY_PATH))
+    lib.fa2_forward_production_128x128.argtypes = [
+        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+        ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+        ctypes.c_int, ctypes.c_void_p,
+    ]
+    lib.fa2_forward_production_128x128.restype = ctypes.c_int
+    lib.fa2_status_string.argtypes = [ctypes.c_int]
+    lib.fa2_status_string.restype = ctypes.c_char_p
+    lib.fa2_abi_version.argtypes = []
+    lib.fa2_abi_version.restype = ctypes.c_int
+    return lib
+
+
+lib = _load()
+
+
+def declared_functions() -> list[str]:
+    """Names of the functions declared in include/fa2_mi355x.h."""
+    text = HEADER_PATH.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(fa2_\w+)\s*\(", text, flags=re.M)
+
+
+def status_string(status: int) -> str:
+    return lib.fa2_status_string(status).decode()
+
+
+def abi_version() -> int:
+    return lib.fa2_abi_version()
+
+
+def forward_production_128x128_raw(query_ptr: int, key_ptr: int, value_ptr: int,
+                                   output_ptr: int, batch: int, heads: int, seq_len: int,
+                                   head_dim: int, causal: bool, stream: int | None) -> int:
+    """Direct call of the C entry point; returns the status code."""
+    return lib.fa2_forward_production_128x128(
+        query_ptr, key_ptr, value_ptr, output_ptr, batch, heads, seq_len, head_dim,
+        1 if causal else 0, stream,
+    )
+
+
+def forward_production_128x128(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                               causal: bool, *, output: torch.Tensor | None = None,
+                               stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """Attention forward through the C ABI on torch tensors (no validation beyond the ABI's)."""
+    if output is None:
+        output = torch.empty_like(query)
+    if stream is None:
+        stream = torch.cuda.current_stream(query.device)
+    batch, heads, seq_len, head_dim = query.shape
+    status = forward_production_128x128_raw(
+        query.data_ptr(), key.data_ptr(), value.data_ptr(), output.data_ptr(),
+        batch, heads, seq_len, head_dim, causal, stream.cuda_stream,
+    )
+    if status != FA2_STATUS_SUCCESS:
+        raise Fa2Error("fa2_forward_production_128x128", status, status_string(status))
+    return output

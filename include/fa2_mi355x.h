@@ -1,0 +1,67 @@
+/*
+ * fa2_mi355x.h - C ABI of the MI355X (gfx950) FlashAttention-2 forward library.
+ *
+ * Library: flash_attention_2_lab_amd/libfa2_mi355x.so (hand-written HIP for gfx950).
+ *
+ * Every entry point takes plain device pointers and sizes; no torch or HIP types
+ * appear in the signatures. Tensors are FP16 (IEEE binary16), row-major
+ * [batch, heads, seq_len, head_dim], contiguous, 16-byte aligned. The output
+ * buffer is written, never read; inputs are read-only. Calls are asynchronous:
+ * the kernel is enqueued on `stream` (a hipStream_t passed as void*; NULL means
+ * the legacy default stream) and no host synchronisation happens.
+ *
+ * Status codes: 0 on success; a positive FA2_STATUS_* value for an argument the
+ * library rejects before touching the GPU; FA2_STATUS_HIP_ERROR_BASE + hipError_t
+ * when the HIP runtime reports a launch error. fa2_status_string() names each.
+ */
+#ifndef FA2_MI355X_H
+#define FA2_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FA2_MI355X_ABI_VERSION 1
+
+enum fa2_status {
+    FA2_STATUS_SUCCESS = 0,
+    FA2_STATUS_NULL_POINTER = 1,        /* non-empty problem with a NULL tensor pointer      */
+    FA2_STATUS_NEGATIVE_DIMENSION = 2,  /* batch, heads, seq_len or head_dim below zero      */
+    FA2_STATUS_BAD_HEAD_DIM = 3,        /* head_dim != 64                                    */
+    FA2_STATUS_BAD_SEQUENCE_LENGTH = 4, /* seq_len not a multiple of the entry's key tile    */
+    FA2_STATUS_MISALIGNED = 5,          /* a tensor pointer is not 16-byte aligned           */
+    FA2_STATUS_TOO_LARGE = 6,           /* launch grid or element count exceeds the kernel's */
+    FA2_STATUS_HIP_ERROR_BASE = 1000    /* + hipError_t from the launch                      */
+};
+
+/*
+ * Fused attention forward, O = softmax(Q K^T / sqrt(64) [+ causal mask]) V.
+ * FP16 in/out, FP32 accumulation and FP32 online softmax; P is rounded to FP16
+ * before the P.V product, the softmax denominator uses FP32 probabilities.
+ * causal != 0 masks key j > query i.
+ *
+ * Replaces tensorcore_attention_forward_production_128x128
+ *   (reference csrc/tensorcore_attention.cu:3191-3203, implementation 2969-3123,
+ *    validation 2731-2823; binding csrc/bindings.cpp:63-68 and 136-140).
+ * Preconditions mirror the reference: head_dim == 64, seq_len % 128 == 0.
+ * batch, heads or seq_len == 0 returns FA2_STATUS_SUCCESS without a launch
+ * (reference csrc/tensorcore_attention.cu:3003-3009).
+ */
+int fa2_forward_production_128x128(const void* query, const void* key, const void* value,
+                                   void* output, int64_t batch, int64_t heads,
+                                   int64_t seq_len, int64_t head_dim, int causal,
+                                   void* stream);
+
+/* Human-readable name of a status code returned by this library (static storage). */
+const char* fa2_status_string(int status);
+
+/* FA2_MI355X_ABI_VERSION of the loaded library. */
+int fa2_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA2_MI355X_H */

@@ -1,0 +1,94 @@
+"""CPU tests of the C ABI library: it loads, exports every declared symbol, and rejects
+bad arguments with the documented status codes before any HIP call is made."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+
+import pytest
+
+import flash_attention_2_lab_amd as fa
+from flash_attention_2_lab_amd import capi
+
+
+def test_library_exports_every_declared_function():
+    declared = capi.declared_functions()
+    assert {"fa2_forward_production_128x128", "fa2_status_string", "fa2_abi_version"} <= set(declared)
+    lib = ctypes.CDLL(str(capi.LIBRARY_PATH))
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in include/fa2_mi355x.h but not exported"
+
+
+def test_abi_version_matches_header():
+    text = capi.HEADER_PATH.read_text()
+    version = int(re.search(r"#define FA2_MI355X_ABI_VERSION (\d+)", text).group(1))
+    assert capi.abi_version() == version == fa.flash_attention_cuda.abi_version
+
+
+def test_status_codes_match_header():
+    text = capi.HEADER_PATH.read_text()
+    for name in ("SUCCESS", "NULL_POINTER", "NEGATIVE_DIMENSION", "BAD_HEAD_DIM",
+                 "BAD_SEQUENCE_LENGTH", "MISALIGNED", "TOO_LARGE", "HIP_ERROR_BASE"):
+        value = int(re.search(rf"FA2_STATUS_{name} = (\d+)", text).group(1))
+        assert getattr(capi, f"FA2_STATUS_{name}") == value
+
+
+@pytest.mark.parametrize("status, text", [
+    (capi.FA2_STATUS_SUCCESS, "success"),
+    (capi.FA2_STATUS_BAD_HEAD_DIM, "head dimension must equal 64"),
+    (capi.FA2_STATUS_BAD_SEQUENCE_LENGTH, "sequence length must be divisible by 128"),
+    (capi.FA2_STATUS_NULL_POINTER, "null tensor pointer"),
+    (capi.FA2_STATUS_MISALIGNED, "tensor pointer not 16-byte aligned"),
+    (999, "unknown status"),
+    (-1, "unknown status"),
+])
+def test_status_strings(status, text):
+    assert capi.status_string(status) == text
+
+
+def _call(batch=1, heads=1, seq_len=128, head_dim=64, ptrs=(0, 0, 0, 0)):
+    q, k, v, o = ptrs
+    return capi.forward_production_128x128_raw(q, k, v, o, batch, heads, seq_len, head_dim,
+                                               False, None)
+
+
+def test_rejects_head_dim_other_than_64():
+    assert _call(head_dim=32) == capi.FA2_STATUS_BAD_HEAD_DIM
+    assert _call(head_dim=128) == capi.FA2_STATUS_BAD_HEAD_DIM
+
+
+@pytest.mark.parametrize("seq_len", [1, 64, 100, 129, 4095])
+def test_rejects_sequence_length_not_multiple_of_128(seq_len):
+    assert _call(seq_len=seq_len) == capi.FA2_STATUS_BAD_SEQUENCE_LENGTH
+
+
+def test_rejects_negative_dimensions():
+    for kwargs in ({"batch": -1}, {"heads": -2}, {"seq_len": -128}, {"head_dim": -64}):
+        assert _call(**kwargs) == capi.FA2_STATUS_NEGATIVE_DIMENSION
+
+
+def test_empty_problem_succeeds_without_pointers():
+    # Reference csrc/tensorcore_attention.cu:3003-3009: empty input returns early.
+    assert _call(batch=0) == capi.FA2_STATUS_SUCCESS
+    assert _call(heads=0) == capi.FA2_STATUS_SUCCESS
+    assert _call(seq_len=0) == capi.FA2_STATUS_SUCCESS
+
+
+def test_empty_problem_still_checks_head_dim():
+    assert _call(batch=0, head_dim=16) == capi.FA2_STATUS_BAD_HEAD_DIM
+
+
+def test_rejects_null_pointers_for_non_empty_problem():
+    assert _call() == capi.FA2_STATUS_NULL_POINTER
+    assert _call(ptrs=(4096, 4096, 0, 4096)) == capi.FA2_STATUS_NULL_POINTER
+
+
+def test_rejects_misaligned_pointers():
+    assert _call(ptrs=(4096, 4096 + 8, 4096, 4096)) == capi.FA2_STATUS_MISALIGNED
+
+
+def test_rejects_problem_beyond_launch_grid():
+    # Rejected on sizes alone; the (never dereferenced) pointers are aligned and non-null.
+    assert _call(seq_len=1 << 31, ptrs=(4096,) * 4) == capi.FA2_STATUS_TOO_LARGE
+    assert _call(batch=1 << 20, heads=1 << 20, ptrs=(4096,) * 4) == capi.FA2_STATUS_TOO_LARGE

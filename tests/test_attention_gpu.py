@@ -1,0 +1,209 @@
+"""GPU parity tests of the HIP FlashAttention-2 forward against the CPU oracle.
+
+Gates:
+* North star: FP16 output within atol 2e-3 + rtol 1e-2 of the FP32 oracle on the
+  same seeded inputs (configs B1 H8 N{128..1024}, chip-filling shapes, golden vectors,
+  sampled rows of B16 H16 N4096 and B2 H32 N16384 sigma=2).
+* Reference test (tests/test_tensorcore_attention.py:301-372): within 3e-2 of SDPA.
+  SDPA is evaluated on the CPU in FP32 on the same inputs.
+Every kernel call goes through the C ABI (directly via ctypes or via the torch
+binding, which calls the same C entry point).
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import flash_attention_2_lab_amd as fa
+from flash_attention_2_lab_amd import capi
+from oracle import attention_reference_fp32, attention_rows_fp32
+
+pytestmark = pytest.mark.gpu
+
+ENTRY = fa.flash_attention_cuda.tensorcore_attention_forward_production_128x128
+ATOL = 2e-3
+RTOL = 1e-2
+GOLDEN = Path(__file__).resolve().parent / "golden" / "attention_fp16_d64.npz"
+
+
+def _inputs(batch, heads, seq_len, seed=0, sigma=1.0):
+    """q, k, v drawn in that order from one seeded CPU generator (FP16, CPU)."""
+    gen = torch.Generator().manual_seed(seed)
+    shape = (batch, heads, seq_len, 64)
+    q = torch.randn(shape, generator=gen)
+    k = torch.randn(shape, generator=gen)
+    v = torch.randn(shape, generator=gen)
+    return (q * sigma).half(), (k * sigma).half(), v.half()
+
+
+def _run(q, k, v, causal):
+    out = ENTRY(q.cuda(), k.cuda(), v.cuda(), causal)
+    torch.cuda.synchronize()
+    return out
+
+
+def _assert_close_to_oracle(actual_fp16, expected_fp32):
+    assert actual_fp16.dtype == torch.float16
+    torch.testing.assert_close(actual_fp16.float().cpu(), expected_fp32, atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("seq_len", [128, 256, 512, 1024])
+def test_configs_b1_h8_match_oracle(seq_len, causal):
+    q, k, v = _inputs(1, 8, seq_len)
+    out = _run(q, k, v, causal)
+    assert out.shape == q.shape and out.is_cuda
+    _assert_close_to_oracle(out, attention_reference_fp32(q, k, v, causal=causal))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("shape", [(1, 64, 1024), (1, 32, 1024), (2, 16, 2048), (3, 5, 384)])
+def test_workgroup_shapes_match_oracle(shape, causal):
+    # Covers the 4-, 2- and 1-wave workgroup variants and a batch*heads that is not a
+    # multiple of the 8-XCD remap.
+    q, k, v = _inputs(*shape, seed=3)
+    out = _run(q, k, v, causal)
+    _assert_close_to_oracle(out, attention_reference_fp32(q, k, v, causal=causal))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("batch, heads, seq_len", [(1, 2, 128), (1, 4, 256), (1, 8, 512), (1, 8, 1024)])
+def test_production_matches_sdpa(batch, heads, seq_len, causal):
+    # Reference tests/test_tensorcore_attention.py:301-372 (seed 0, randn on the GPU).
+    torch.manual_seed(0)
+    shape = (batch, heads, seq_len, 64)
+    q = torch.randn(shape, device="cuda", dtype=torch.float16).contiguous()
+    k = torch.randn(shape, device="cuda", dtype=torch.float16).contiguous()
+    v = torch.randn(shape, device="cuda", dtype=torch.float16).contiguous()
+    expected = F.scaled_dot_product_attention(q.float().cpu(), k.float().cpu(), v.float().cpu(),
+                                              attn_mask=None, dropout_p=0.0, is_causal=causal).half()
+    actual = ENTRY(q, k, v, causal)
+    assert actual.shape == expected.shape
+    assert actual.dtype == torch.float16
+    assert actual.is_cuda
+    torch.testing.assert_close(actual.cpu(), expected, rtol=3e-2, atol=3e-2)
+
+
+def test_golden_vectors_through_binding_and_c_abi():
+    with np.load(GOLDEN) as data:
+        arrays = {name: data[name] for name in data.files}
+    cases = sorted({name.split("/")[0] for name in arrays})
+    checked = 0
+    for case in cases:
+        q, k, v = (torch.from_numpy(arrays[f"{case}/{t}"]).cuda() for t in ("query", "key", "value"))
+        for mode in ("noncausal", "causal"):
+            if f"{case}/{mode}" not in arrays:
+                continue
+            causal = mode == "causal"
+            expected = torch.from_numpy(arrays[f"{case}/{mode}"])
+            via_binding = ENTRY(q, k, v, causal)
+            via_c_abi = capi.forward_production_128x128(q, k, v, causal)
+            torch.cuda.synchronize()
+            _assert_close_to_oracle(via_binding, expected)
+            assert torch.equal(via_binding, via_c_abi), f"{case}/{mode}: binding and C ABI differ"
+            checked += 1
+    assert checked >= 5
+
+
+def _sample_rows(batch, heads, seq_len, count, seed):
+    gen = torch.Generator().manual_seed(seed)
+    rows = {(0, 0, 0), (0, 0, 1), (batch - 1, heads - 1, seq_len - 1), (0, heads - 1, 127),
+            (batch - 1, 0, 128), (0, 0, 63), (0, 0, 64)}
+    while len(rows) < count:
+        b = int(torch.randint(batch, (1,), generator=gen))
+        h = int(torch.randint(heads, (1,), generator=gen))
+        i = int(torch.randint(seq_len, (1,), generator=gen))
+        rows.add((b, h, i))
+    return sorted(rows)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_throughput_shape_b16_h16_n4096(causal):
+    q, k, v = _inputs(16, 16, 4096)
+    out = _run(q, k, v, causal).cpu()
+    assert torch.isfinite(out).all()
+    rows = _sample_rows(16, 16, 4096, 192, seed=11)
+    expected = attention_rows_fp32(q, k, v, rows, causal=causal)
+    actual = torch.stack([out[b, h, i] for b, h, i in rows])
+    _assert_close_to_oracle(actual, expected)
+    if causal:
+        assert torch.equal(out[:, :, 0], v[:, :, 0])
+
+
+def test_long_context_b2_h32_n16384_sigma2_causal():
+    q, k, v = _inputs(2, 32, 16384, seed=0, sigma=2.0)
+    out = _run(q, k, v, True).cpu()
+    assert torch.isfinite(out).all()
+    rows = _sample_rows(2, 32, 16384, 128, seed=12)
+    expected = attention_rows_fp32(q, k, v, rows, causal=True)
+    actual = torch.stack([out[b, h, i] for b, h, i in rows])
+    _assert_close_to_oracle(actual, expected)
+    assert torch.equal(out[:, :, 0], v[:, :, 0])
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_constant_value_gives_constant_output(causal):
+    q, k, _ = _inputs(2, 4, 512, seed=5)
+    v = torch.full_like(q, 0.8125)
+    out = _run(q, k, v, causal).float().cpu()
+    torch.testing.assert_close(out, torch.full_like(out, 0.8125), atol=ATOL, rtol=RTOL)
+
+
+def test_repeat_calls_are_bitwise_identical_and_inputs_untouched():
+    q, k, v = (t.cuda() for t in _inputs(2, 8, 1024, seed=6))
+    q0, k0, v0 = q.clone(), k.clone(), v.clone()
+    a = ENTRY(q, k, v, True)
+    b = ENTRY(q, k, v, True)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    assert torch.equal(q, q0) and torch.equal(k, k0) and torch.equal(v, v0)
+
+
+def test_runs_on_the_current_stream():
+    q, k, v = (t.cuda() for t in _inputs(1, 8, 512, seed=7))
+    expected = ENTRY(q, k, v, False)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        out = ENTRY(q, k, v, False)
+        via_c_abi = capi.forward_production_128x128(q, k, v, False)
+    side.synchronize()
+    assert torch.equal(out, expected)
+    assert torch.equal(via_c_abi, expected)
+
+
+@pytest.mark.parametrize("shape", [(0, 2, 128, 64), (1, 0, 128, 64), (2, 3, 0, 64)])
+def test_empty_inputs_return_empty_output(shape):
+    x = torch.empty(shape, device="cuda", dtype=torch.float16)
+    out = ENTRY(x, x, x, True)
+    assert out.shape == x.shape and out.dtype == torch.float16 and out.is_cuda
+
+
+@pytest.mark.parametrize("mutate, message", [
+    (lambda q, k, v: (q.float(), k, v), "query must have dtype torch.float16"),
+    (lambda q, k, v: (q, k, v[:, :1]), "query and value must have identical shapes"),
+    (lambda q, k, v: (q.transpose(1, 2).contiguous().transpose(1, 2), k, v), "query must be contiguous"),
+    (lambda q, k, v: (q[..., :32].contiguous(), k[..., :32].contiguous(), v[..., :32].contiguous()),
+     "head dimension must equal 64"),
+    (lambda q, k, v: (q[:, :, :64].contiguous(), k[:, :, :64].contiguous(), v[:, :, :64].contiguous()),
+     "sequence length must be divisible by 128"),
+    (lambda q, k, v: (q, k.cpu(), v), "key must be a CUDA tensor"),
+])
+def test_validation_on_gpu_tensors(mutate, message):
+    q, k, v = (t.cuda() for t in _inputs(1, 2, 128))
+    with pytest.raises(RuntimeError, match=message):
+        ENTRY(*mutate(q, k, v), False)
+
+
+def test_c_abi_rejects_misaligned_device_pointer_without_launch():
+    buf = torch.zeros(2 * 128 * 64 + 8, device="cuda", dtype=torch.float16)
+    ptr = buf.data_ptr()
+    status = capi.forward_production_128x128_raw(ptr + 2, ptr, ptr, ptr, 1, 1, 128, 64, False,
+                                                 torch.cuda.current_stream().cuda_stream)
+    assert status == capi.FA2_STATUS_MISALIGNED

@@ -93,6 +93,28 @@ def roofline(flops, avg_s):
             "unit": "TFLOP/s", "frac": round(achieved / MI355X_FP16_DENSE_TFLOPS, 5), "traffic": None}
 
 
+# Workloads of the benchmark configurations: (batch, heads, seq_len, sigma).
+WORKLOADS = {
+    "b1h8n1024": (1, 8, 1024, 1.0),
+    "b16h16n4096": (16, 16, 4096, 1.0),
+    "b2h32n16384": (2, 32, 16384, 2.0),
+}
+
+
+def run_single(entry, args):
+    """Times one workload (used under rocprofv3); prints one JSON line."""
+    batch, heads, seq_len, sigma = WORKLOADS[args.only]
+    modes = {"noncausal": (False,), "causal": (True,), "both": (False, True)}[args.mode]
+    inputs = make_inputs(batch, heads, seq_len, sigma=sigma, device="cuda")
+    _, per_kernel = time_kernel_batches(entry, inputs, modes, args.steps, args.warmup)
+    out = {"workload": args.only, "steps": args.steps}
+    for mode, avg in per_kernel.items():
+        f = attention_flops(batch, heads, seq_len, 64, mode == "causal")
+        out[mode] = {"us": round(avg * 1e6, 3), "tflops": round(f / avg / 1e12, 2)}
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def cpu_baseline(budget_s):
     """Oracle (FP32 torch restatement of the reference) on this host's CPU cores."""
     import torch
@@ -128,6 +150,9 @@ def main() -> int:
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--skip-north-star", action="store_true")
     parser.add_argument("--skip-cpu", action="store_true")
+    parser.add_argument("--only", choices=sorted(WORKLOADS),
+                        help="time one workload only (for profilers); prints its own JSON line")
+    parser.add_argument("--mode", choices=("noncausal", "causal", "both"), default="both")
     args = parser.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -143,6 +168,9 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
     entry = fa.flash_attention_cuda.tensorcore_attention_forward_production_128x128
+
+    if args.only:
+        return run_single(entry, args)
 
     modes = (False, True)
     inputs = make_inputs(1, 8, 1024, device="cuda")

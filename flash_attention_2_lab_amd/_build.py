@@ -46,6 +46,12 @@ HIP_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the softmax reads and rescales them with VALU ops,
+    # which AGPR accumulators would force through v_accvgpr_read/write copies.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
+    # The kernels never produce NaN; this lets fmaxf chains become v_max3_f32
+    # without canonicalisation.
+    "-fno-honor-nans",
     "-Wno-unused-command-line-argument",
 ]
 

@@ -18,10 +18,13 @@
 //    (LDS transpose read), so K and V are staged identically.
 //  * O^T lives in the MFMA accumulators: every accumulator of a lane belongs to the
 //    lane's own query, so the online-softmax rescale needs no cross-lane traffic.
-//  * K/V tiles (64 keys x 64 dims, 8 KiB each) are double-buffered in LDS with a
-//    16-byte-chunk XOR swizzle that keeps both the K reads (ds_read_b128) and the
-//    V transpose reads free of bank conflicts; tile j+1 is prefetched into
-//    registers while tile j is computed, one barrier per tile.
+//  * K/V tiles (64 keys x 64 dims, 8 KiB each) stream through four LDS stages by
+//    direct-to-LDS buffer loads (no staging registers), fetched three tiles ahead
+//    of use with one barrier per tile. A 16-byte-chunk XOR swizzle, applied on the
+//    global side of the DMA, keeps the K reads (ds_read_b128) and the V transpose
+//    reads free of bank conflicts.
+//  * Software pipeline inside each wave: the scores of tile j+1 are computed
+//    while the softmax of tile j runs, so MFMA and VALU work overlap.
 //  * Causal mode stops the key loop at the diagonal, skips tiles a wave can never
 //    see and masks only diagonal tiles (key > query -> -inf).
 //  * Workgroup ids are remapped so all query tiles of one (batch, head) land on the
@@ -32,6 +35,8 @@
 #include <stdint.h>
 #include <math.h>
 
+#include <type_traits>
+
 #include "fa2_mi355x.h"
 
 namespace {
@@ -40,9 +45,10 @@ constexpr int kHeadDim = 64;
 constexpr int kQueriesPerWave = 32;
 constexpr int kKeysPerTile = 64;                          // BN
 constexpr int kRowBytes = kHeadDim * 2;                   // 128 B per key row
-constexpr int kChunksPerTile = kKeysPerTile * kRowBytes / 16;  // 512 chunks of 16 B
 constexpr int kTileBytes = kKeysPerTile * kRowBytes;      // 8 KiB
 constexpr int kQueryTileAlign = 128;                      // reference kProductionBlockM/N
+constexpr float kRescaleLog2 = 8.0f;                      // lazy-rescale threshold, log2 units
+constexpr int64_t kMaxSeqLen = (int64_t)1 << 24;          // seq_len * 128 B fits in int32
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
@@ -55,14 +61,20 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 #define FA2_LDS __attribute__((address_space(3)))
 
-// XOR applied to the 16-byte chunk index of key row `row` inside an LDS tile.
-// Bits: chunk ^= ((row & 3) << 1) | ((row >> 3) & 1).
-//  - K reads (A operand of K*Q^T): 8 consecutive lanes read rows sigma(8g..8g+7),
-//    whose bits {0,1,3} take all 8 values -> 8 distinct chunks, 128 B, no conflict.
-//  - V transpose reads: a 16-lane group reads rows 4a..4a+3 at one 32-byte
-//    column pair; (row & 3) << 1 moves each row to a different pair.
+// XOR applied to the 16-byte chunk index of key row `row` inside an LDS tile:
+// chunk ^= b3 | (b0 ^ b2) << 1 | b1 << 2, with b_k bit k of the row. A tile row is
+// 128 B; the mask keeps every LDS access of the kernel free of bank conflicts for
+// 32 banks (128 B per pass) and for 64 banks (256 B per pass):
+//  - K reads (ds_read_b128, A operand of K*Q^T): a pass covers MFMA rows 8g..8g+7
+//    (or 16g..16g+15), i.e. key rows sigma(.) whose bits {0,1,3} (or {0,1,2,3})
+//    take every value; the mask maps them to distinct (row parity, chunk) slots.
+//  - V transpose reads (ds_read_b64_tr_b16): a 16-lane group reads rows 4a..4a+3
+//    at one 32-byte column pair, two groups read the 4 pairs of one 64-byte quad;
+//    bits 1-2 of the mask move the 4 rows to 4 pairs and b1 moves rows of equal
+//    parity to opposite quads.
+//  - Tile fills are LDS-DMA writes of 1 KiB contiguous per instruction.
 __device__ __forceinline__ int tile_swizzle(int row) {
-    return ((row & 3) << 1) | ((row >> 3) & 1);
+    return ((row >> 3) & 1) | (((row ^ (row >> 2)) & 1) << 1) | (((row >> 1) & 1) << 2);
 }
 
 // MFMA row r of a 32-key block reads key sigma(r): bits 2 and 3 of r swapped.
@@ -92,45 +104,71 @@ __device__ __forceinline__ f16x4 lds_read_transposed(const uint8_t* p) {
     return __builtin_bit_cast(f16x4, r);
 }
 
-// Registers that carry one 64x64 FP16 tile from global memory to LDS.
-template <int kThreads>
-struct TileCarrier {
-    static constexpr int kPerThread = kChunksPerTile / kThreads;
-    static_assert(kChunksPerTile % kThreads == 0, "tile chunks must split evenly");
-    u32x4 r[kPerThread];
+// Empty register constraint: the value must be computed before this point.
+template <typename T>
+__device__ __forceinline__ void pin_vgprs(T& v) {
+    asm volatile("" : "+v"(v));
+}
 
-    __device__ __forceinline__ void load(const uint8_t* __restrict__ src, int tid) {
-#pragma unroll
-        for (int i = 0; i < kPerThread; ++i) {
-            const int c = tid + i * kThreads;
-            r[i] = *reinterpret_cast<const u32x4*>(src + (c >> 3) * kRowBytes + (c & 7) * 16);
-        }
-    }
+// Buffer resource over one head's [seq_len, 64] FP16 slab (gfx9 descriptor word 3).
+// Buffer loads take the slab base from SGPRs and a 32-bit per-lane offset, and
+// return zeros outside num_records instead of faulting.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t head_resource(const void* base, int seq_len) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                            seq_len * kRowBytes, 0x00020000);
+}
 
-    __device__ __forceinline__ void store(uint8_t* dst, int tid) const {
-#pragma unroll
-        for (int i = 0; i < kPerThread; ++i) {
-            const int c = tid + i * kThreads;
-            const int row = c >> 3;
-            *reinterpret_cast<u32x4*>(dst + row * kRowBytes + (((c & 7) ^ tile_swizzle(row)) << 4)) =
-                r[i];
-        }
-    }
-};
+// One LDS-DMA instruction (buffer_load_dwordx4 ... lds) moves 1 KiB: rows r0..r0+7
+// of a K or V tile. Lane i writes LDS row r0 + i/8, chunk i%8 (the hardware writes
+// lane i at M0 + 16*i), so it reads the global chunk the swizzle places there:
+// logical chunk (i%8) ^ tile_swizzle(r0 + i/8). `lane_offset` is that lane's byte
+// offset relative to row r0; it depends on r0 only through bit 3 of the row.
+__device__ __forceinline__ int dma_lane_offset(int lane, int r0_bit3) {
+    const int row = (lane >> 3) | (r0_bit3 << 3);
+    return (lane >> 3) * kRowBytes + (((lane & 7) ^ tile_swizzle(row)) << 4);
+}
+
+__device__ __forceinline__ void dma_rows(__amdgpu_buffer_rsrc_t src, uint8_t* lds_rows,
+                                         int lane_offset, int src_offset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (FA2_LDS void*)lds_rows, 16, lane_offset,
+                                             src_offset, 0, 0);
+}
+
+// Waits until at most `kPending` vector-memory instructions of this wave are in
+// flight and its LDS reads are done, then joins the workgroup barrier. The caller
+// passes the number of LDS-DMA instructions issued after the tile it needs.
+template <int kPending>
+__device__ __forceinline__ void wait_dma_and_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kPending) : "memory");
+}
 
 template <bool kCausal, int kWaves>
 __global__ __launch_bounds__(kWaves * 64)
+__attribute__((amdgpu_waves_per_eu(kWaves == 4 ? 2 : 1)))  // 4-wave groups: two waves per SIMD
 void fa2_forward_d64_kernel(const _Float16* __restrict__ query,
                             const _Float16* __restrict__ key,
                             const _Float16* __restrict__ value,
                             _Float16* __restrict__ output,
                             int seq_len, int num_query_tiles, float scale_log2) {
-    constexpr int kThreads = kWaves * 64;
     constexpr int kBlockM = kWaves * kQueriesPerWave;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[2][2][kTileBytes];  // [buffer][K|V]
+    // Tile t (K then V, 16 KiB) lives in stage t % 4. Iteration j reads V of tile j
+    // and K of tile j+1, tile j+2 is landing and tile j+3 is being fetched, so the
+    // fetch runs two iterations ahead of its use with one barrier per tile. Four
+    // separate arrays let the compiler see that a fetch and a read of another stage
+    // are independent.
+    constexpr int kStageBytes = 2 * kTileBytes;
+    constexpr int kDmaPerTile = 2 * kTileBytes / 1024 / kWaves;  // LDS-DMA instructions per wave
+    __shared__ __attribute__((aligned(1024))) uint8_t stage0[kStageBytes];
+    __shared__ __attribute__((aligned(1024))) uint8_t stage1[kStageBytes];
+    __shared__ __attribute__((aligned(1024))) uint8_t stage2[kStageBytes];
+    __shared__ __attribute__((aligned(1024))) uint8_t stage3[kStageBytes];
+    auto stage_at = [&](int st) -> uint8_t* {
+        return st == 0 ? stage0 : st == 1 ? stage1 : st == 2 ? stage2 : stage3;
+    };
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
+    // Wave index in an SGPR: it selects buffer descriptors and LDS-DMA bases.
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
     const int lq = lane & 31;   // query column owned by this lane
     const int half = lane >> 5; // which 16 of each 32 keys this lane holds
@@ -150,13 +188,37 @@ void fa2_forward_d64_kernel(const _Float16* __restrict__ query,
 
     const size_t head_offset = (size_t)bh * (size_t)seq_len * kHeadDim;
     const _Float16* __restrict__ q_head = query + head_offset;
-    const uint8_t* __restrict__ k_head = reinterpret_cast<const uint8_t*>(key + head_offset);
-    const uint8_t* __restrict__ v_head = reinterpret_cast<const uint8_t*>(value + head_offset);
+    const __amdgpu_buffer_rsrc_t k_head = head_resource(key + head_offset, seq_len);
+    const __amdgpu_buffer_rsrc_t v_head = head_resource(value + head_offset, seq_len);
     _Float16* __restrict__ o_head = output + head_offset;
 
     const int q_block = (int)qtile * kBlockM;
     const int q_wave = q_block + wave * kQueriesPerWave;
     const int my_query = q_wave + lq;
+
+    // Key tiles the workgroup streams, and the last one this wave can see.
+    const int num_tiles = kCausal ? (q_block + kBlockM - 1) / kKeysPerTile + 1
+                                  : seq_len / kKeysPerTile;
+    const int wave_last_tile = kCausal ? (q_wave + kQueriesPerWave - 1) / kKeysPerTile
+                                       : num_tiles - 1;
+
+    // LDS-DMA of tile t into a stage: this wave issues instructions n = wave + x*kWaves
+    // of the 16 (8 per matrix, 8 rows each).
+    const int dma_off[2] = {dma_lane_offset(lane, 0), dma_lane_offset(lane, 1)};
+    auto dma_tile = [&](int t, uint8_t* stage) {
+#pragma unroll
+        for (int x = 0; x < kDmaPerTile; ++x) {
+            const int n = wave + x * kWaves;
+            const int m = n >> 3;
+            const int r0 = (n & 7) * 8;
+            dma_rows(m ? v_head : k_head, stage + m * kTileBytes + r0 * kRowBytes, dma_off[n & 1],
+                     t * kTileBytes + r0 * kRowBytes);
+        }
+    };
+    // Tiles 0..2 start landing while Q is loaded.
+    dma_tile(0, stage0);
+    if (num_tiles > 1) dma_tile(1, stage1);
+    if (num_tiles > 2) dma_tile(2, stage2);
 
     // Q^T as the B operand of K*Q^T: lane holds dims 16ks + 8*half + 0..7 of its query.
     f16x8 q_frag[4];
@@ -165,11 +227,9 @@ void fa2_forward_d64_kernel(const _Float16* __restrict__ query,
         q_frag[ks] = *reinterpret_cast<const f16x8*>(q_head + (size_t)my_query * kHeadDim +
                                                       ks * 16 + half * 8);
 
-    const int num_tiles = kCausal ? (q_block + kBlockM - 1) / kKeysPerTile + 1
-                                  : seq_len / kKeysPerTile;
-
     // Per-lane LDS byte offsets.
-    // K (A operand): MFMA row lq -> key row sigma(lq) (+32 for block 1), chunk 2ks + half.
+    // K (A operand): MFMA row lq reads key row sigma(lq) (+32 rows for block 1) at
+    // chunk 2ks + half.
     const int k_row = key_of_mfma_row(lq);
     const int k_swz = tile_swizzle(k_row);
     int k_off[4];
@@ -177,17 +237,19 @@ void fa2_forward_d64_kernel(const _Float16* __restrict__ query,
     for (int ks = 0; ks < 4; ++ks) k_off[ks] = k_row * kRowBytes + (((2 * ks + half) ^ k_swz) << 4);
     // V^T (A operand) through transpose reads. In a 16-lane group g, lane i reads 4
     // halves at key row base + i/4, dims d0 + 4*(i%4); the read returns, to lane i,
-    // dim d0 + i at keys base..base+3. Row base = 32b + 16t + 8*half + 4r.
+    // dim d0 + i at keys base..base+3. Row base = 32b + 16t + 8*half + 4r; the
+    // swizzle of that row depends on the lane and on r only.
     const int grp = lane >> 4;
     const int i16 = lane & 15;
-    const int v_row = 8 * half + (i16 >> 2);
-    const int v_swz = ((i16 >> 2) << 1) | half;  // tile_swizzle(v_row + 32b + 16t + 4r)
-    int v_off[2];
+    int v_off[2][2];  // [r][dblk]
 #pragma unroll
-    for (int dblk = 0; dblk < 2; ++dblk) {
-        const int chunk = 4 * dblk + 2 * (grp & 1) + ((i16 & 3) >> 1);
-        v_off[dblk] = v_row * kRowBytes + ((chunk ^ v_swz) << 4) + 8 * (i16 & 1);
-    }
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int dblk = 0; dblk < 2; ++dblk) {
+            const int row = 8 * half + 4 * r + (i16 >> 2);
+            const int chunk = 4 * dblk + 2 * (grp & 1) + ((i16 & 3) >> 1);
+            v_off[r][dblk] = row * kRowBytes + ((chunk ^ tile_swizzle(row)) << 4) + 8 * (i16 & 1);
+        }
 
     f32x16 o_acc[2];
 #pragma unroll
@@ -196,111 +258,242 @@ void fa2_forward_d64_kernel(const _Float16* __restrict__ query,
         for (int i = 0; i < 16; ++i) o_acc[d][i] = 0.0f;
     float m_run = -INFINITY;  // running max of raw scores (unscaled) for my_query
     float l_run = 0.0f;       // this lane's share of the running softmax denominator
+    const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
 
-    TileCarrier<kThreads> k_carry, v_carry;
-    k_carry.load(k_head, tid);
-    v_carry.load(v_head, tid);
-    k_carry.store(&smem[0][0][0], tid);
-    v_carry.store(&smem[0][1][0], tid);
-    __syncthreads();
+    // K fragments of a tile: block b (keys 32b..32b+31), k-step ks (dims 16ks..16ks+15).
+    auto load_k = [&](const uint8_t* k_lds, f16x8 (&kf)[2][4]) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+                kf[b][ks] = *reinterpret_cast<const f16x8*>(k_lds + b * 32 * kRowBytes + k_off[ks]);
+    };
+    // V^T fragment of P.V MFMA k of a tile: block k/4, 16-key half (k/2)%2, d-block k%2.
+    auto load_v = [&](const uint8_t* v_lds, int k) -> f16x8 {
+        const int row_base = (32 * (k >> 2) + 16 * ((k >> 1) & 1)) * kRowBytes;
+        const f16x4 v_lo = lds_read_transposed(v_lds + row_base + v_off[0][k & 1]);
+        const f16x4 v_hi = lds_read_transposed(v_lds + row_base + v_off[1][k & 1]);
+        return __builtin_shufflevector(v_lo, v_hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    };
+    // S^T MFMA k of a tile: block k%2, k-step k/2 (the block's chain starts at k < 2).
+    auto score_mfma = [&](const f16x8 (&kf)[2][4], int k, f32x16 (&s)[2]) {
+        const f32x16 zero = {};
+        const int b = k & 1, ks = k >> 1;
+        s[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[b][ks], q_frag[ks], ks == 0 ? zero : s[b], 0, 0, 0);
+    };
 
-    for (int j = 0; j < num_tiles; ++j) {
-        const int buf = j & 1;
-        const bool has_next = j + 1 < num_tiles;
-        if (has_next) {
-            k_carry.load(k_head + (size_t)(j + 1) * kTileBytes, tid);
-            v_carry.load(v_head + (size_t)(j + 1) * kTileBytes, tid);
+    // Causal mask of tile t: register i of block b holds key 64t + 32b + 16(i/8) +
+    // 8*half + i%8; keys after my_query become -inf. Only tiles that reach past the
+    // wave's first query need it.
+    auto mask = [&](int t, f32x16 (&s)[2]) {
+        if (!kCausal || t * kKeysPerTile + kKeysPerTile - 1 <= q_wave) return;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int key_index = t * kKeysPerTile + 32 * b + 16 * (i >> 3) + 8 * half + (i & 7);
+                if (key_index > my_query) s[b][i] = -INFINITY;
+            }
+    };
+
+    // Lazy rescale: the running max moves only when some query's tile max exceeds
+    // it by more than kRescaleLog2 (log2 units), so probabilities stay below
+    // 2^kRescaleLog2 and O, l share one (possibly stale) max - O / l is unchanged.
+    // The first tile always moves it (m_run = -inf gives alpha = 0). l is rescaled
+    // here; O by the caller (rarely needed: behind a wave-uniform branch placed where
+    // O is not being accumulated). Returns whether O needs it and sets `alpha`.
+    auto decide_rescale = [&](float tile_max, float& alpha) -> bool {
+        tile_max = max_across_halves(tile_max);
+        const bool grow = tile_max * scale_log2 > m_run * scale_log2 + kRescaleLog2;
+        const bool any_grow = __builtin_amdgcn_ballot_w64(grow) != 0;
+        const float m_new = any_grow ? fmaxf(m_run, tile_max) : m_run;
+        alpha = m_new == m_run ? 1.0f : __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
+        l_run *= alpha;
+        m_run = m_new;
+        return any_grow;
+    };
+    auto partial_max = [&](const f32x16& sb, int i0, int n, float m) {
+#pragma unroll
+        for (int i = 0; i < n; i += 2) m = fmaxf(fmaxf(m, sb[i0 + i]), sb[i0 + i + 1]);
+        return m;
+    };
+    auto rescale_o = [&](float alpha) {
+#pragma unroll
+        for (int d = 0; d < 2; ++d)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o_acc[d][i] *= alpha;
+    };
+
+    // One exp pair: p = 2^(s*scale*log2e - m*scale*log2e) for accumulator registers
+    // 2q, 2q+1 of a block, rounded to FP16 (nearest) and added to the row sum
+    // (v_dot2_f32_f16 against 1.0, so the sum adds the FP16 values the MFMA uses).
+    auto exp_pair = [&](const f32x16& sb, int q, float m_scaled, f16x2 (&pk)[8], float& sum) {
+        pk[q] = pack_rn(__builtin_amdgcn_exp2f(fmaf(sb[2 * q], scale_log2, -m_scaled)),
+                        __builtin_amdgcn_exp2f(fmaf(sb[2 * q + 1], scale_log2, -m_scaled)));
+        sum = __builtin_amdgcn_fdot2(pk[q], ones, sum, false);
+    };
+    // The 8 pairs of a block as the B operands of its two P.V MFMAs (16 keys each).
+    auto assemble = [&](const f16x2 (&pk)[8], f16x8 (&p)[2]) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const f16x4 lo = __builtin_shufflevector(pk[4 * t], pk[4 * t + 1], 0, 1, 2, 3);
+            const f16x4 hi = __builtin_shufflevector(pk[4 * t + 2], pk[4 * t + 3], 0, 1, 2, 3);
+            p[t] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         }
-        const int k0 = j * kKeysPerTile;
-        // Causal: a wave whose last query precedes the tile sees none of it.
-        const bool active = !kCausal || k0 <= q_wave + kQueriesPerWave - 1;
+    };
+    auto exp_block = [&](const f32x16& sb, float m_scaled, f16x8 (&p)[2]) {
+        f16x2 pk[8];
+        float sum = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) exp_pair(sb, q, m_scaled, pk, sum);
+        l_run += sum;
+        assemble(pk, p);
+    };
+
+    // Prologue: tiles 0 and 1 landed; scores, max and block-0 P of tile 0.
+    __syncthreads();  // waits for every outstanding DMA (tiles 0..2) and Q
+    f32x16 s_a[2], s_b[2];
+    f16x8 p_lo[2];  // FP16 P of block 0 of the tile being finished
+    {
+        f16x8 kf[2][4];
+        load_k(stage0, kf);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) score_mfma(kf, k, s_a);
+        mask(0, s_a);
+        float alpha;
+        const float tile_max = partial_max(s_a[1], 0, 16, partial_max(s_a[0], 0, 16, -INFINITY));
+        if (decide_rescale(tile_max, alpha)) rescale_o(alpha);
+        exp_block(s_a[0], m_run * scale_log2, p_lo);
+    }
+
+    // Iteration j finishes tile j (cur) and starts tile j+1 (next) in two phases of
+    // eight MFMAs, each with independent VALU work beside it:
+    //   phase 1: S^T of tile j+1 (8 MFMAs)      | exp of block 1 of tile j
+    //   phase 2: P.V of tile j (8 MFMAs)        | row max of tile j+1, exp of its block 0
+    //
+    // Steady state: tiles j and j+1 are unmasked and seen by every wave and tile j+3
+    // exists. Stages are compile-time (j % 4 == kStage); the order of MFMA, VALU and
+    // LDS reads is fixed by scheduling fences, one MFMA per slot.
+    auto steady = [&](int j, auto stage_tag, f32x16 (&cur)[2], f32x16 (&next)[2]) {
+        constexpr int kStage = decltype(stage_tag)::value;
+        uint8_t* const st_cur = kStage == 0 ? stage0 : kStage == 1 ? stage1 : kStage == 2 ? stage2 : stage3;
+        uint8_t* const st_next = kStage == 3 ? stage0 : kStage == 0 ? stage1 : kStage == 1 ? stage2 : stage3;
+        uint8_t* const st_fetch = kStage == 1 ? stage0 : kStage == 2 ? stage1 : kStage == 3 ? stage2 : stage3;
+        dma_tile(j + 3, st_fetch);
+        f16x8 kf[2][4];
+        load_k(st_next, kf);
+        const uint8_t* v_lds = st_cur + kTileBytes;
+        __builtin_amdgcn_sched_barrier(0);
+
+        // Phase 1: slot k = score MFMA k of tile j+1 + exp pair k of block 1 of tile
+        // j + the transpose reads of P.V MFMA k of tile j.
+        const float m_cur = m_run * scale_log2;
+        f16x2 pk_hi[8];
+        float sum_hi = 0.0f;
+        f16x8 vf[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            score_mfma(kf, k, next);
+            exp_pair(cur[1], k, m_cur, pk_hi, sum_hi);
+            vf[k] = load_v(v_lds, k);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        l_run += sum_hi;
+        f16x8 p_hi[2];
+        assemble(pk_hi, p_hi);
+
+        // Phase 2: P.V MFMAs of tile j (block 0 with p_lo, block 1 with p_hi), beside
+        // the row max of tile j+1 (slots 0-3) and the exp of its block 0 (slots 4-7).
+        float tile_max = -INFINITY;
+        float alpha = 1.0f;
+        bool grew = false;
+        float m_next = 0.0f;
+        f16x2 pk_lo[8];
+        float sum_lo = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const f16x8& pf = (k < 4) ? p_lo[(k >> 1) & 1] : p_hi[(k >> 1) & 1];
+            o_acc[k & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[k], pf, o_acc[k & 1], 0, 0, 0);
+            if (k < 4) {
+                tile_max = partial_max(next[k >> 1], 8 * (k & 1), 8, tile_max);
+                if (k == 3) {
+                    grew = decide_rescale(tile_max, alpha);
+                    m_next = m_run * scale_log2;
+                }
+            } else {
+                exp_pair(next[0], 2 * (k - 4), m_next, pk_lo, sum_lo);
+                exp_pair(next[0], 2 * (k - 4) + 1, m_next, pk_lo, sum_lo);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        l_run += sum_lo;
+        assemble(pk_lo, p_lo);
+        // Materialise the next tile's P here: without this the compiler sinks the
+        // phase-2 exps past the rescale branch, out of their MFMA slots.
+        pin_vgprs(p_lo[0]);
+        pin_vgprs(p_lo[1]);
+        pin_vgprs(l_run);
+        if (grew) rescale_o(alpha);
+        // Tile j+2 must have landed (only tile j+3's DMAs may be in flight).
+        wait_dma_and_barrier<kDmaPerTile>();
+    };
+
+    // Any iteration: the last tiles, causal diagonal tiles, tiles a wave of a causal
+    // workgroup does not see, and steady iterations that do not start a group of 4.
+    auto generic = [&](int j, f32x16 (&cur)[2], f32x16 (&next)[2]) {
+        const bool active = j <= wave_last_tile;
+        const bool next_active = j + 1 < num_tiles && j + 1 <= wave_last_tile;
+        if (j + 3 < num_tiles) dma_tile(j + 3, stage_at((j + 3) & 3));
+        const uint8_t* v_lds = stage_at(j & 3) + kTileBytes;
+        f16x8 p_hi[2];
         if (active) {
-            const uint8_t* k_lds = &smem[buf][0][0];
-            const uint8_t* v_lds = &smem[buf][1][0];
-
-            // S^T = K Q^T for two 32-key blocks.
-            f32x16 s[2];
 #pragma unroll
-            for (int b = 0; b < 2; ++b) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) s[b][i] = 0.0f;
-#pragma unroll
-                for (int ks = 0; ks < 4; ++ks) {
-                    const f16x8 kf = *reinterpret_cast<const f16x8*>(k_lds + b * 32 * kRowBytes + k_off[ks]);
-                    s[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, q_frag[ks], s[b], 0, 0, 0);
-                }
-            }
-
-            // Accumulator register i of block b holds key k0 + 32b + 16(i/8) + 8*half + i%8.
-            if (kCausal && k0 + kKeysPerTile - 1 > q_wave) {
-#pragma unroll
-                for (int b = 0; b < 2; ++b)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const int key_index = k0 + 32 * b + 16 * (i >> 3) + 8 * half + (i & 7);
-                        if (key_index > my_query) s[b][i] = -INFINITY;
-                    }
-            }
-
-            float tile_max = -INFINITY;
-#pragma unroll
-            for (int b = 0; b < 2; ++b)
-#pragma unroll
-                for (int i = 0; i < 16; i += 2) tile_max = fmaxf(tile_max, fmaxf(s[b][i], s[b][i + 1]));
-            tile_max = max_across_halves(tile_max);
-            const float m_new = fmaxf(m_run, tile_max);
-            // m_run == -inf only before the first tile, where the correction is 0.
-            const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
-            const float m_scaled = m_new * scale_log2;
-
-            // p = exp(scale * (s - m)) = 2^(s * scale*log2e - m * scale*log2e).
-            float p_sum = 0.0f;
-            f16x8 p_frag[2][2];
-#pragma unroll
-            for (int b = 0; b < 2; ++b)
-#pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    float p[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        p[e] = __builtin_amdgcn_exp2f(fmaf(s[b][8 * t + e], scale_log2, -m_scaled));
-                        p_sum += p[e];
-                    }
-                    const f16x2 p01 = pack_rn(p[0], p[1]);
-                    const f16x2 p23 = pack_rn(p[2], p[3]);
-                    const f16x2 p45 = pack_rn(p[4], p[5]);
-                    const f16x2 p67 = pack_rn(p[6], p[7]);
-                    const f16x4 lo = __builtin_shufflevector(p01, p23, 0, 1, 2, 3);
-                    const f16x4 hi = __builtin_shufflevector(p45, p67, 0, 1, 2, 3);
-                    p_frag[b][t] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-                }
-            l_run = l_run * alpha + p_sum;
-            m_run = m_new;
-#pragma unroll
-            for (int d = 0; d < 2; ++d)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) o_acc[d][i] *= alpha;
-
-            // O^T += V^T P^T, 16 keys per MFMA.
-#pragma unroll
-            for (int b = 0; b < 2; ++b)
-#pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    const int row_base = (32 * b + 16 * t) * kRowBytes;
-#pragma unroll
-                    for (int dblk = 0; dblk < 2; ++dblk) {
-                        const f16x4 v_lo = lds_read_transposed(v_lds + row_base + v_off[dblk]);
-                        const f16x4 v_hi = lds_read_transposed(v_lds + row_base + 4 * kRowBytes + v_off[dblk]);
-                        const f16x8 vf = __builtin_shufflevector(v_lo, v_hi, 0, 1, 2, 3, 4, 5, 6, 7);
-                        o_acc[dblk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, p_frag[b][t], o_acc[dblk], 0, 0, 0);
-                    }
-                }
+            for (int k = 0; k < 4; ++k)
+                o_acc[k & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(load_v(v_lds, k), p_lo[(k >> 1) & 1], o_acc[k & 1], 0, 0, 0);
+            exp_block(cur[1], m_run * scale_log2, p_hi);
         }
-        if (has_next) {
-            k_carry.store(&smem[buf ^ 1][0][0], tid);
-            v_carry.store(&smem[buf ^ 1][1][0], tid);
+        if (next_active) {
+            f16x8 kf[2][4];
+            load_k(stage_at((j + 1) & 3), kf);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) score_mfma(kf, k, next);
         }
-        __syncthreads();
+        if (active) {
+#pragma unroll
+            for (int k = 4; k < 8; ++k)
+                o_acc[k & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(load_v(v_lds, k), p_hi[(k >> 1) & 1], o_acc[k & 1], 0, 0, 0);
+        }
+        if (next_active) {
+            mask(j + 1, next);
+            float alpha;
+            const float tile_max = partial_max(next[1], 0, 16, partial_max(next[0], 0, 16, -INFINITY));
+            if (decide_rescale(tile_max, alpha)) rescale_o(alpha);
+            exp_block(next[0], m_run * scale_log2, p_lo);
+        }
+        __syncthreads();  // waits for every outstanding DMA
+    };
+
+    // Steady iterations need tiles j, j+1 unmasked for wave 0 (the workgroup's first
+    // query) and tile j+3 present; they run in groups of four from j = 0 so that
+    // j % 4 (the stage) is known at compile time.
+    const int first_masked_tile = kCausal ? q_block / kKeysPerTile : num_tiles;
+    const int steady_end = max(0, min(first_masked_tile - 1, num_tiles - 3));
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using S2 = std::integral_constant<int, 2>;
+    using S3 = std::integral_constant<int, 3>;
+    int j = 0;
+    for (; j + 4 <= steady_end; j += 4) {
+        steady(j, S0{}, s_a, s_b);
+        steady(j + 1, S1{}, s_b, s_a);
+        steady(j + 2, S2{}, s_a, s_b);
+        steady(j + 3, S3{}, s_b, s_a);
+    }
+    bool flipped = false;
+    for (; j < num_tiles; ++j) {
+        if (flipped) generic(j, s_b, s_a);
+        else generic(j, s_a, s_b);
+        flipped = !flipped;
     }
 
     // Epilogue: O = O^T / l. Accumulator i of d-block dblk holds dim
@@ -357,8 +550,9 @@ extern "C" int fa2_forward_production_128x128(const void* query, const void* key
     if (!query || !key || !value || !output) return FA2_STATUS_NULL_POINTER;
     if (misaligned(query) || misaligned(key) || misaligned(value) || misaligned(output))
         return FA2_STATUS_MISALIGNED;
-    // Kernel indexing: seq_len and the query-tile count are int, the grid is 1-D.
-    if (seq_len > (int64_t)INT32_MAX || batch > (int64_t)UINT32_MAX / heads)
+    // Kernel indexing: byte offsets inside one head's slab are 32-bit (buffer
+    // loads), the grid is 1-D.
+    if (seq_len > kMaxSeqLen || batch > (int64_t)UINT32_MAX / heads)
         return FA2_STATUS_TOO_LARGE;
     const int64_t batch_heads = batch * heads;
     if (batch_heads > (int64_t)UINT32_MAX / (seq_len / kQueriesPerWave)) return FA2_STATUS_TOO_LARGE;

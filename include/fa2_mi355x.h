@@ -32,7 +32,7 @@ enum fa2_status {
     FA2_STATUS_BAD_HEAD_DIM = 3,        /* head_dim != 64                                    */
     FA2_STATUS_BAD_SEQUENCE_LENGTH = 4, /* seq_len not a multiple of the entry's key tile    */
     FA2_STATUS_MISALIGNED = 5,          /* a tensor pointer is not 16-byte aligned           */
-    FA2_STATUS_TOO_LARGE = 6,           /* launch grid or element count exceeds the kernel's */
+    FA2_STATUS_TOO_LARGE = 6,           /* seq_len > 2^24 or launch grid beyond 2^32 groups */
     FA2_STATUS_HIP_ERROR_BASE = 1000    /* + hipError_t from the launch                      */
 };
 

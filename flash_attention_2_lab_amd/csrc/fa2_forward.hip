@@ -511,6 +511,279 @@ void fa2_forward_d64_kernel(const _Float16* __restrict__ query,
         }
 }
 
+// LDS-DMA through inline assembly: M0 = LDS destination of lane 0 (wave-uniform),
+// then buffer_load_dwordx4 ... lds. The compiler does not track these loads, so it
+// adds no waits for them; the kernel waits with explicit vmcnt.
+__device__ __forceinline__ void dma16_asm(u32x4 src, uint32_t lds_addr, int lane_offset,
+                                          int src_offset) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :: "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(lane_offset), "s"(src),
+                    "s"(__builtin_amdgcn_readfirstlane(src_offset))
+                 : "memory", "m0");
+}
+
+// Buffer descriptor (base, stride 0, num_records, gfx9 word 3) in SGPRs, as an
+// inline-assembly operand.
+__device__ __forceinline__ u32x4 head_descriptor(const void* base, int seq_len) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    u32x4 d;
+    d[0] = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    d[1] = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu);
+    d[2] = (uint32_t)(seq_len * kRowBytes);
+    d[3] = 0x00020000u;
+    return d;
+}
+
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+    return (uint32_t)(uintptr_t)(FA2_LDS const void*)p;
+}
+
+// Key-split variant for problems too small to fill the chip with 128-query
+// workgroups. A workgroup owns one 32-query block; its 4 waves each stream a
+// quarter of the key tiles that block sees, through two LDS stages of their own
+// (each wave fetches and reads only its own stages, so the key loop has no
+// workgroup barrier), and keep their own running max, sum and O. At the end the
+// four partial results are merged through LDS:
+//   m = max_w m_w,  l = sum_w l_w 2^((m_w - m) s log2e),  O = sum_w O_w 2^(...) / l.
+template <bool kCausal>
+__global__ __launch_bounds__(256) void fa2_forward_splitk_kernel(const _Float16* __restrict__ query,
+                                                                 const _Float16* __restrict__ key,
+                                                                 const _Float16* __restrict__ value,
+                                                                 _Float16* __restrict__ output,
+                                                                 int seq_len, int num_query_blocks,
+                                                                 float scale_log2) {
+    constexpr int kSplit = 4;
+    constexpr int kStageBytes = 2 * kTileBytes;             // K tile then V tile
+    constexpr int kDmaPerTile = 2 * kTileBytes / 1024;      // one wave fetches whole tiles
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kSplit * 2 * kStageBytes];
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int lq = lane & 31;
+    const int half = lane >> 5;
+
+    // Workgroup -> (batch*head, query block), XCD-contiguous; causal blocks run
+    // heaviest first.
+    const uint32_t groups = gridDim.x;
+    const uint32_t xcd = blockIdx.x & 7u;
+    const uint32_t slot = blockIdx.x >> 3;
+    const uint32_t per_xcd = groups >> 3;
+    const uint32_t extra = groups & 7u;
+    const uint32_t logical = xcd * per_xcd + min(xcd, extra) + slot;
+    const uint32_t bh = logical / (uint32_t)num_query_blocks;
+    uint32_t qblock = logical - bh * (uint32_t)num_query_blocks;
+    if (kCausal) qblock = (uint32_t)num_query_blocks - 1u - qblock;
+
+    const size_t head_offset = (size_t)bh * (size_t)seq_len * kHeadDim;
+    const _Float16* __restrict__ q_head = query + head_offset;
+    const u32x4 k_head = head_descriptor(key + head_offset, seq_len);
+    const u32x4 v_head = head_descriptor(value + head_offset, seq_len);
+    _Float16* __restrict__ o_head = output + head_offset;
+
+    const int q0 = (int)qblock * kQueriesPerWave;
+    const int my_query = q0 + lq;
+    const int visible_tiles = kCausal ? (q0 + kQueriesPerWave - 1) / kKeysPerTile + 1
+                                      : seq_len / kKeysPerTile;
+    const int t_begin = wave * visible_tiles / kSplit;
+    const int t_end = (wave + 1) * visible_tiles / kSplit;
+
+    uint8_t* const my_stages = smem + wave * 2 * kStageBytes;
+    const uint32_t my_stages_addr = lds_address(my_stages);
+    const int dma_off[2] = {dma_lane_offset(lane, 0), dma_lane_offset(lane, 1)};
+    auto dma_tile = [&](int t, int st) {
+#pragma unroll
+        for (int n = 0; n < kDmaPerTile; ++n) {
+            const int m = n >> 3;
+            const int r0 = (n & 7) * 8;
+            dma16_asm(m ? v_head : k_head,
+                      my_stages_addr + (uint32_t)(st * kStageBytes + m * kTileBytes + r0 * kRowBytes),
+                      dma_off[n & 1], t * kTileBytes + r0 * kRowBytes);
+        }
+    };
+
+    f16x8 q_frag[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+        q_frag[ks] = *reinterpret_cast<const f16x8*>(q_head + (size_t)my_query * kHeadDim +
+                                                      ks * 16 + half * 8);
+    if (t_begin < t_end) dma_tile(t_begin, 0);
+
+    const int k_row = key_of_mfma_row(lq);
+    const int k_swz = tile_swizzle(k_row);
+    int k_off[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) k_off[ks] = k_row * kRowBytes + (((2 * ks + half) ^ k_swz) << 4);
+    const int grp = lane >> 4;
+    const int i16 = lane & 15;
+    int v_off[2][2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int dblk = 0; dblk < 2; ++dblk) {
+            const int row = 8 * half + 4 * r + (i16 >> 2);
+            const int chunk = 4 * dblk + 2 * (grp & 1) + ((i16 & 3) >> 1);
+            v_off[r][dblk] = row * kRowBytes + ((chunk ^ tile_swizzle(row)) << 4) + 8 * (i16 & 1);
+        }
+
+    f32x16 o_acc[2];
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o_acc[d][i] = 0.0f;
+    float m_run = -INFINITY;
+    float l_run = 0.0f;
+    const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+
+    for (int t = t_begin; t < t_end; ++t) {
+        const int st = (t - t_begin) & 1;
+        if (t + 1 < t_end) {
+            dma_tile(t + 1, st ^ 1);
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerTile) : "memory");  // tile t landed
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        const uint8_t* k_lds = my_stages + st * kStageBytes;
+        const uint8_t* v_lds = k_lds + kTileBytes;
+
+        // S^T = K Q^T for the tile's two 32-key blocks.
+        f16x8 kf[2][4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+                kf[b][ks] = *reinterpret_cast<const f16x8*>(k_lds + b * 32 * kRowBytes + k_off[ks]);
+        f32x16 sc[2];
+        const f32x16 zero = {};
+#pragma unroll
+        for (int b = 0; b < 2; ++b) sc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[b][0], q_frag[0], zero, 0, 0, 0);
+#pragma unroll
+        for (int ks = 1; ks < 4; ++ks)
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+                sc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[b][ks], q_frag[ks], sc[b], 0, 0, 0);
+
+        if (kCausal && t * kKeysPerTile + kKeysPerTile - 1 > q0) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int key_index = t * kKeysPerTile + 32 * b + 16 * (i >> 3) + 8 * half + (i & 7);
+                    if (key_index > my_query) sc[b][i] = -INFINITY;
+                }
+        }
+
+        // Online softmax with the lazy rescale (bound 2^kRescaleLog2).
+        float tile_max = -INFINITY;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int i = 0; i < 16; i += 2) tile_max = fmaxf(fmaxf(tile_max, sc[b][i]), sc[b][i + 1]);
+        tile_max = max_across_halves(tile_max);
+        const bool grow = tile_max * scale_log2 > m_run * scale_log2 + kRescaleLog2;
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+            const float m_new = fmaxf(m_run, tile_max);
+            const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
+            l_run *= alpha;
+#pragma unroll
+            for (int d = 0; d < 2; ++d)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o_acc[d][i] *= alpha;
+            m_run = m_new;
+        }
+        const float m_scaled = m_run * scale_log2;
+        f16x8 pf[2][2];
+        float sum0 = 0.0f, sum1 = 0.0f;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            f16x2 pk[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                pk[q] = pack_rn(__builtin_amdgcn_exp2f(fmaf(sc[b][2 * q], scale_log2, -m_scaled)),
+                                __builtin_amdgcn_exp2f(fmaf(sc[b][2 * q + 1], scale_log2, -m_scaled)));
+                if (q & 1) sum1 = __builtin_amdgcn_fdot2(pk[q], ones, sum1, false);
+                else sum0 = __builtin_amdgcn_fdot2(pk[q], ones, sum0, false);
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const f16x4 lo = __builtin_shufflevector(pk[4 * h], pk[4 * h + 1], 0, 1, 2, 3);
+                const f16x4 hi = __builtin_shufflevector(pk[4 * h + 2], pk[4 * h + 3], 0, 1, 2, 3);
+                pf[b][h] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            }
+        }
+        l_run += sum0 + sum1;
+
+        // O^T += V^T P^T.
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int row_base = (32 * (k >> 2) + 16 * ((k >> 1) & 1)) * kRowBytes;
+            const f16x4 v_lo = lds_read_transposed(v_lds + row_base + v_off[0][k & 1]);
+            const f16x4 v_hi = lds_read_transposed(v_lds + row_base + v_off[1][k & 1]);
+            const f16x8 vf = __builtin_shufflevector(v_lo, v_hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            o_acc[k & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[k >> 2][(k >> 1) & 1], o_acc[k & 1], 0, 0, 0);
+        }
+    }
+
+    // Merge the four partial results (stages are free once every wave is done).
+    __syncthreads();
+    float* red_o = reinterpret_cast<float*>(smem);                  // [wave][8][64 lanes][4]
+    float* red_m = red_o + kSplit * 8 * 64 * 4;                      // [wave][64]
+    float* red_l = red_m + kSplit * 64;                              // [wave][64]
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = o_acc[j >> 2][4 * (j & 3) + e];
+        *reinterpret_cast<f32x4*>(red_o + ((wave * 8 + j) * 64 + lane) * 4) = v;
+    }
+    red_m[wave * 64 + lane] = m_run;
+    red_l[wave * 64 + lane] = sum_across_halves(l_run);
+    __syncthreads();
+    if (wave != 0) return;
+
+    float m_tot = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kSplit; ++w) m_tot = fmaxf(m_tot, red_m[w * 64 + lane]);
+    float weight[kSplit];
+    float l_tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kSplit; ++w) {
+        const float m_w = red_m[w * 64 + lane];
+        // A wave that saw no keys has m_w = -inf, l_w = 0, O_w = 0: weight 0.
+        weight[w] = m_w == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_w - m_tot) * scale_log2);
+        l_tot += red_l[w * 64 + lane] * weight[w];
+    }
+    const float inv_l = 1.0f / l_tot;
+    _Float16* o_row = o_head + (size_t)my_query * kHeadDim;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        f32x4 acc = {};
+#pragma unroll
+        for (int w = 0; w < kSplit; ++w) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(red_o + ((w * 8 + j) * 64 + lane) * 4);
+            acc += v * weight[w];
+        }
+        // Float j holds dims 32*(j/4) + 8*(j%4) + 4*half + 0..3 of my_query.
+        const f16x2 a = pack_rn(acc[0] * inv_l, acc[1] * inv_l);
+        const f16x2 c = pack_rn(acc[2] * inv_l, acc[3] * inv_l);
+        *reinterpret_cast<f16x4*>(o_row + 32 * (j >> 2) + 8 * (j & 3) + 4 * half) =
+            __builtin_shufflevector(a, c, 0, 1, 2, 3);
+    }
+}
+
+template <bool kCausal>
+hipError_t launch_splitk(const void* q, const void* k, const void* v, void* o,
+                         int64_t batch_heads, int64_t seq_len, float scale_log2,
+                         hipStream_t stream) {
+    const int64_t query_blocks = seq_len / kQueriesPerWave;
+    hipLaunchKernelGGL((fa2_forward_splitk_kernel<kCausal>), dim3((unsigned)(batch_heads * query_blocks)),
+                       dim3(256), 0, stream,
+                       static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
+                       static_cast<const _Float16*>(v), static_cast<_Float16*>(o),
+                       (int)seq_len, (int)query_blocks, scale_log2);
+    return hipGetLastError();
+}
+
 template <bool kCausal, int kWaves>
 hipError_t launch_forward(const void* q, const void* k, const void* v, void* o,
                           int64_t batch_heads, int64_t seq_len, float scale_log2,
@@ -526,13 +799,11 @@ hipError_t launch_forward(const void* q, const void* k, const void* v, void* o,
     return hipGetLastError();
 }
 
-// Queries per workgroup: 128 (4 waves) when the grid fills the chip, fewer waves per
-// workgroup for small problems so that more CUs get work.
+// 128-query workgroups (4 waves) when they fill the chip (two per CU); otherwise
+// the key-split kernel (one 32-query block per workgroup, keys split over 4 waves).
 int choose_waves(int64_t batch_heads, int64_t seq_len) {
     constexpr int64_t kTargetGroups = 512;  // 2 per CU on 256 CUs
-    if (batch_heads * (seq_len / 128) >= kTargetGroups) return 4;
-    if (batch_heads * (seq_len / 64) >= kTargetGroups) return 2;
-    return 1;
+    return batch_heads * (seq_len / 128) >= kTargetGroups ? 4 : 1;
 }
 
 bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) != 0; }
@@ -562,14 +833,12 @@ extern "C" int fa2_forward_production_128x128(const void* query, const void* key
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int waves = choose_waves(batch_heads, seq_len);
     hipError_t err;
-    if (causal) {
-        err = waves == 4   ? launch_forward<true, 4>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
-              : waves == 2 ? launch_forward<true, 2>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
-                           : launch_forward<true, 1>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
+    if (waves == 4) {
+        err = causal ? launch_forward<true, 4>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
+                     : launch_forward<false, 4>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
     } else {
-        err = waves == 4   ? launch_forward<false, 4>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
-              : waves == 2 ? launch_forward<false, 2>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
-                           : launch_forward<false, 1>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
+        err = causal ? launch_splitk<true>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
+                     : launch_splitk<false>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
     }
     return err == hipSuccess ? FA2_STATUS_SUCCESS : FA2_STATUS_HIP_ERROR_BASE + (int)err;
 }

@@ -87,10 +87,25 @@ def time_kernel_batches(entry, inputs, modes, steps, warmup):
     return wall, per_kernel
 
 
-def roofline(flops, avg_s):
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
+
+
+def measured_traffic(key):
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
+    (calibrated on a plain copy), or None when that workload was not profiled."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            entry = json.load(f)["kernels"].get(key)
+    except (OSError, ValueError, KeyError):
+        return None
+    return None if entry is None else entry["hbm_bytes"]
+
+
+def roofline(flops, avg_s, traffic_key=None):
     achieved = flops / avg_s / 1e12
     return {"bound": "mfma", "achieved": round(achieved, 3), "peak": MI355X_FP16_DENSE_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(achieved / MI355X_FP16_DENSE_TFLOPS, 5), "traffic": None}
+            "unit": "TFLOP/s", "frac": round(achieved / MI355X_FP16_DENSE_TFLOPS, 5),
+            "traffic": measured_traffic(traffic_key) if traffic_key else None}
 
 
 # Workloads of the benchmark configurations: (batch, heads, seq_len, sigma).
@@ -101,8 +116,36 @@ WORKLOADS = {
 }
 
 
+# Plain device-to-device copy of a known size: calibrates the FETCH_SIZE and
+# WRITE_SIZE counters (each should read this many bytes per dispatch).
+COPY_CALIBRATION_BYTES = 256 << 20
+
+
+def run_copy_calibration(args):
+    import torch
+
+    src = torch.empty(COPY_CALIBRATION_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(args.warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    avg = e0.elapsed_time(e1) / 1e3 / args.steps
+    print(json.dumps({"workload": "copy", "bytes_per_copy": COPY_CALIBRATION_BYTES,
+                      "us": round(avg * 1e6, 3),
+                      "GBps": round(2 * COPY_CALIBRATION_BYTES / avg / 1e9, 1)}), flush=True)
+    return 0
+
+
 def run_single(entry, args):
     """Times one workload (used under rocprofv3); prints one JSON line."""
+    if args.only == "copy":
+        return run_copy_calibration(args)
     batch, heads, seq_len, sigma = WORKLOADS[args.only]
     modes = {"noncausal": (False,), "causal": (True,), "both": (False, True)}[args.mode]
     inputs = make_inputs(batch, heads, seq_len, sigma=sigma, device="cuda")
@@ -150,7 +193,7 @@ def main() -> int:
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--skip-north-star", action="store_true")
     parser.add_argument("--skip-cpu", action="store_true")
-    parser.add_argument("--only", choices=sorted(WORKLOADS),
+    parser.add_argument("--only", choices=sorted(WORKLOADS) + ["copy"],
                         help="time one workload only (for profilers); prints its own JSON line")
     parser.add_argument("--mode", choices=("noncausal", "causal", "both"), default="both")
     args = parser.parse_args()
@@ -199,7 +242,8 @@ def main() -> int:
                    "batch": 1, "heads": 8, "seq_len": 1024, "head_dim": 64,
                    "baseline_hardware": "RTX 4070 Laptop (reference README.md:21-42)"},
         "us": {m: round(t * 1e6, 3) for m, t in per_kernel.items()},
-        "roofline": dict(roofline(flops_by_mode[dominant], per_kernel[dominant]), kernel=dominant,
+        "roofline": dict(roofline(flops_by_mode[dominant], per_kernel[dominant], f"b1h8n1024/{dominant}"),
+                         kernel=dominant,
                          hbm_frac=round(attention_bytes(1, 8, 1024, 64) / per_kernel[dominant]
                                         / 1e9 / MI355X_HBM_GBPS, 5)),
     }
@@ -212,7 +256,7 @@ def main() -> int:
         for mode, avg in t.items():
             f = attention_flops(16, 16, 4096, 64, mode == "causal")
             north[f"B16H16N4096_{mode}"] = {"us": round(avg * 1e6, 2), "tflops": round(f / avg / 1e12, 2),
-                                            "roofline": roofline(f, avg)}
+                                            "roofline": roofline(f, avg, f"b16h16n4096/{mode}")}
         del big
         long_ctx = make_inputs(2, 32, 16384, sigma=2.0, device="cuda")
         _, t = time_kernel_batches(entry, long_ctx, (True,), max(3, args.north_star_steps // 4), 1)

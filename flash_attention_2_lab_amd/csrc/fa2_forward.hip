@@ -104,12 +104,6 @@ __device__ __forceinline__ f16x4 lds_read_transposed(const uint8_t* p) {
     return __builtin_bit_cast(f16x4, r);
 }
 
-// Empty register constraint: the value must be computed before this point.
-template <typename T>
-__device__ __forceinline__ void pin_vgprs(T& v) {
-    asm volatile("" : "+v"(v));
-}
-
 // Buffer resource over one head's [seq_len, 64] FP16 slab (gfx9 descriptor word 3).
 // Buffer loads take the slab base from SGPRs and a 32-bit per-lane offset, and
 // return zeros outside num_records instead of faulting.
@@ -341,19 +335,37 @@ void fa2_forward_d64_kernel(const _Float16* __restrict__ query,
             p[t] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         }
     };
-    auto exp_block = [&](const f32x16& sb, float m_scaled, f16x8 (&p)[2]) {
-        f16x2 pk[8];
+    // Probabilities are computed against the running max before the tile's own max
+    // is known (the "stale" max). A lane's probabilities are all <= 2^kRescaleLog2
+    // when their sum is, so one compare of the tile's row sum replaces the row max
+    // in the common case; only when some lane's sum exceeds the bound is the exact
+    // tile max taken (decide_rescale) and the tile's probabilities recomputed.
+    constexpr float kTileSumBound = 256.0f;  // 2^kRescaleLog2
+    static_assert(kRescaleLog2 == 8.0f, "kTileSumBound is 2^kRescaleLog2");
+    // Redo tile `s` after a failed check: exact max, rescale of l and O, and both
+    // blocks' probabilities against the new max. Returns the tile's lane sum.
+    auto refresh_tile = [&](const f32x16 (&s)[2], f16x8 (&p0)[2], f16x8 (&p1)[2], float tile_sum) -> float {
+        float alpha;
+        const float tile_max = partial_max(s[1], 0, 16, partial_max(s[0], 0, 16, -INFINITY));
+        if (!decide_rescale(tile_max, alpha)) return tile_sum;  // every probability is <= 2^8
+        rescale_o(alpha);
+        const float m_scaled = m_run * scale_log2;
         float sum = 0.0f;
+        f16x2 pk[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) exp_pair(sb, q, m_scaled, pk, sum);
-        l_run += sum;
-        assemble(pk, p);
+        for (int q = 0; q < 8; ++q) exp_pair(s[0], q, m_scaled, pk, sum);
+        assemble(pk, p0);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) exp_pair(s[1], q, m_scaled, pk, sum);
+        assemble(pk, p1);
+        return sum;
     };
 
-    // Prologue: tiles 0 and 1 landed; scores, max and block-0 P of tile 0.
+    // Prologue: tiles 0..2 landed; scores, exact max and block-0 P of tile 0.
     __syncthreads();  // waits for every outstanding DMA (tiles 0..2) and Q
     f32x16 s_a[2], s_b[2];
-    f16x8 p_lo[2];  // FP16 P of block 0 of the tile being finished
+    f16x8 p_lo[2];        // FP16 P of block 0 of the tile being finished
+    float sum_lo = 0.0f;  // its lane sum, not yet in l_run
     {
         f16x8 kf[2][4];
         load_k(stage0, kf);
@@ -363,13 +375,17 @@ void fa2_forward_d64_kernel(const _Float16* __restrict__ query,
         float alpha;
         const float tile_max = partial_max(s_a[1], 0, 16, partial_max(s_a[0], 0, 16, -INFINITY));
         if (decide_rescale(tile_max, alpha)) rescale_o(alpha);
-        exp_block(s_a[0], m_run * scale_log2, p_lo);
+        f16x2 pk[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) exp_pair(s_a[0], q, m_run * scale_log2, pk, sum_lo);
+        assemble(pk, p_lo);
     }
 
     // Iteration j finishes tile j (cur) and starts tile j+1 (next) in two phases of
-    // eight MFMAs, each with independent VALU work beside it:
-    //   phase 1: S^T of tile j+1 (8 MFMAs)      | exp of block 1 of tile j
-    //   phase 2: P.V of tile j (8 MFMAs)        | row max of tile j+1, exp of its block 0
+    // eight MFMAs, each slot with one exp pair beside its MFMA:
+    //   phase 1: S^T of tile j+1 (8 MFMAs)  | exp of block 1 of tile j, V^T reads of tile j
+    //   check of tile j (rarely: exact max and recompute)
+    //   phase 2: P.V of tile j (8 MFMAs)    | exp of block 0 of tile j+1
     //
     // Steady state: tiles j and j+1 are unmasked and seen by every wave and tile j+3
     // exists. Stages are compile-time (j % 4 == kStage); the order of MFMA, VALU and
@@ -385,55 +401,45 @@ void fa2_forward_d64_kernel(const _Float16* __restrict__ query,
         const uint8_t* v_lds = st_cur + kTileBytes;
         __builtin_amdgcn_sched_barrier(0);
 
-        // Phase 1: slot k = score MFMA k of tile j+1 + exp pair k of block 1 of tile
-        // j + the transpose reads of P.V MFMA k of tile j.
+        // Phase 1: slot k = score MFMA k of tile j+1 (block 0's chain first, so it is
+        // complete before phase 2 reads it) + exp pair k of block 1 of tile j + the
+        // transpose reads of P.V MFMA k of tile j.
+        // Phase 1 runs at raised wave priority: its MFMAs are independent of
+        // the other wave's softmax, so the arbiter should favour them.
+        __builtin_amdgcn_s_setprio(1);
         const float m_cur = m_run * scale_log2;
         f16x2 pk_hi[8];
         float sum_hi = 0.0f;
         f16x8 vf[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            score_mfma(kf, k, next);
+            score_mfma(kf, ((k & 3) << 1) | (k >> 2), next);
             exp_pair(cur[1], k, m_cur, pk_hi, sum_hi);
             vf[k] = load_v(v_lds, k);
             __builtin_amdgcn_sched_barrier(0);
         }
-        l_run += sum_hi;
         f16x8 p_hi[2];
         assemble(pk_hi, p_hi);
+        float tile_sum = sum_lo + sum_hi;
+        if (__builtin_amdgcn_ballot_w64(tile_sum > kTileSumBound) != 0)
+            tile_sum = refresh_tile(cur, p_lo, p_hi, tile_sum);
+        l_run += tile_sum;
+        __builtin_amdgcn_sched_barrier(0);
 
-        // Phase 2: P.V MFMAs of tile j (block 0 with p_lo, block 1 with p_hi), beside
-        // the row max of tile j+1 (slots 0-3) and the exp of its block 0 (slots 4-7).
-        float tile_max = -INFINITY;
-        float alpha = 1.0f;
-        bool grew = false;
-        float m_next = 0.0f;
+        __builtin_amdgcn_s_setprio(0);
+        // Phase 2: P.V MFMAs of tile j (block 0 with p_lo, block 1 with p_hi) beside
+        // the exp of block 0 of tile j+1 against the current max.
+        const float m_next = m_run * scale_log2;
         f16x2 pk_lo[8];
-        float sum_lo = 0.0f;
+        sum_lo = 0.0f;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const f16x8& pf = (k < 4) ? p_lo[(k >> 1) & 1] : p_hi[(k >> 1) & 1];
             o_acc[k & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[k], pf, o_acc[k & 1], 0, 0, 0);
-            if (k < 4) {
-                tile_max = partial_max(next[k >> 1], 8 * (k & 1), 8, tile_max);
-                if (k == 3) {
-                    grew = decide_rescale(tile_max, alpha);
-                    m_next = m_run * scale_log2;
-                }
-            } else {
-                exp_pair(next[0], 2 * (k - 4), m_next, pk_lo, sum_lo);
-                exp_pair(next[0], 2 * (k - 4) + 1, m_next, pk_lo, sum_lo);
-            }
+            exp_pair(next[0], k, m_next, pk_lo, sum_lo);
             __builtin_amdgcn_sched_barrier(0);
         }
-        l_run += sum_lo;
         assemble(pk_lo, p_lo);
-        // Materialise the next tile's P here: without this the compiler sinks the
-        // phase-2 exps past the rescale branch, out of their MFMA slots.
-        pin_vgprs(p_lo[0]);
-        pin_vgprs(p_lo[1]);
-        pin_vgprs(l_run);
-        if (grew) rescale_o(alpha);
         // Tile j+2 must have landed (only tile j+3's DMAs may be in flight).
         wait_dma_and_barrier<kDmaPerTile>();
     };
@@ -445,30 +451,34 @@ void fa2_forward_d64_kernel(const _Float16* __restrict__ query,
         const bool next_active = j + 1 < num_tiles && j + 1 <= wave_last_tile;
         if (j + 3 < num_tiles) dma_tile(j + 3, stage_at((j + 3) & 3));
         const uint8_t* v_lds = stage_at(j & 3) + kTileBytes;
-        f16x8 p_hi[2];
         if (active) {
+            f16x2 pk[8];
+            float sum_hi = 0.0f;
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
-                o_acc[k & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(load_v(v_lds, k), p_lo[(k >> 1) & 1], o_acc[k & 1], 0, 0, 0);
-            exp_block(cur[1], m_run * scale_log2, p_hi);
+            for (int q = 0; q < 8; ++q) exp_pair(cur[1], q, m_run * scale_log2, pk, sum_hi);
+            f16x8 p_hi[2];
+            assemble(pk, p_hi);
+            float tile_sum = sum_lo + sum_hi;
+            if (__builtin_amdgcn_ballot_w64(tile_sum > kTileSumBound) != 0)
+                tile_sum = refresh_tile(cur, p_lo, p_hi, tile_sum);
+            l_run += tile_sum;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const f16x8& pf = (k < 4) ? p_lo[(k >> 1) & 1] : p_hi[(k >> 1) & 1];
+                o_acc[k & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(load_v(v_lds, k), pf, o_acc[k & 1], 0, 0, 0);
+            }
         }
         if (next_active) {
             f16x8 kf[2][4];
             load_k(stage_at((j + 1) & 3), kf);
 #pragma unroll
             for (int k = 0; k < 8; ++k) score_mfma(kf, k, next);
-        }
-        if (active) {
-#pragma unroll
-            for (int k = 4; k < 8; ++k)
-                o_acc[k & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(load_v(v_lds, k), p_hi[(k >> 1) & 1], o_acc[k & 1], 0, 0, 0);
-        }
-        if (next_active) {
             mask(j + 1, next);
-            float alpha;
-            const float tile_max = partial_max(next[1], 0, 16, partial_max(next[0], 0, 16, -INFINITY));
-            if (decide_rescale(tile_max, alpha)) rescale_o(alpha);
-            exp_block(next[0], m_run * scale_log2, p_lo);
+            f16x2 pk[8];
+            sum_lo = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) exp_pair(next[0], q, m_run * scale_log2, pk, sum_lo);
+            assemble(pk, p_lo);
         }
         __syncthreads();  // waits for every outstanding DMA
     };
@@ -513,7 +523,11 @@ void fa2_forward_d64_kernel(const _Float16* __restrict__ query,
 
 // LDS-DMA through inline assembly: M0 = LDS destination of lane 0 (wave-uniform),
 // then buffer_load_dwordx4 ... lds. The compiler does not track these loads, so it
-// adds no waits for them; the kernel waits with explicit vmcnt.
+// adds no waits for them; the kernel waits with explicit vmcnt. M0 is a reserved
+// register that the compiler sets before each of its own uses, so listing it as
+// clobbered is only documentation (clang warns about reserved clobbers).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16_asm(u32x4 src, uint32_t lds_addr, int lane_offset,
                                           int src_offset) {
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
@@ -521,6 +535,7 @@ __device__ __forceinline__ void dma16_asm(u32x4 src, uint32_t lds_addr, int lane
                     "s"(__builtin_amdgcn_readfirstlane(src_offset))
                  : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // Buffer descriptor (base, stride 0, num_records, gfx9 word 3) in SGPRs, as an
 // inline-assembly operand.

@@ -147,6 +147,21 @@ def test_long_context_b2_h32_n16384_sigma2_causal():
 
 
 @pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("shape", [(1, 64, 1024), (1, 8, 1024)])
+def test_growing_scores_match_oracle(shape, causal):
+    # Key norms ramp up 5x along the sequence, so the running max keeps growing and
+    # the kernels' stale-max probabilities overflow the tile-sum bound tile after
+    # tile: exercises the exact-max recompute path (both the 128-query and the
+    # key-split kernels).
+    q, k, v = _inputs(*shape, seed=9)
+    ramp = torch.linspace(1.0, 5.0, shape[2]).view(1, 1, -1, 1)
+    k = (k.float() * ramp).half()
+    out = _run(q, k, v, causal)
+    assert torch.isfinite(out).all()
+    _assert_close_to_oracle(out, attention_reference_fp32(q, k, v, causal=causal))
+
+
+@pytest.mark.parametrize("causal", [False, True])
 def test_constant_value_gives_constant_output(causal):
     q, k, _ = _inputs(2, 4, 512, seed=5)
     v = torch.full_like(q, 0.8125)

@@ -11,7 +11,7 @@ Drop-in for the operator surface of joshprinzel/flash_attention_2_lab:
 
 The compute path is hand-written HIP for gfx950 (``csrc/fa2_forward.hip``); there is
 no CPU or PyTorch fallback. If the built libraries are missing the import fails;
-build them with ``python -m flash_attention_2_lab_amd._build``.
+build them with ``python flash_attention_2_lab_amd/_build.py``.
 """
 
 from __future__ import annotations
@@ -27,7 +27,7 @@ try:
 except ImportError as exc:  # pragma: no cover - exercised only on an unbuilt tree
     raise ImportError(
         "flash_attention_2_lab_amd: the HIP extension is not built "
-        "(run `python -m flash_attention_2_lab_amd._build`)"
+        "(run `python flash_attention_2_lab_amd/_build.py`)"
     ) from exc
 
 from . import capi

@@ -12,7 +12,8 @@ Both are plain compiler invocations (hipcc cross-compiles gfx950 without a GPU);
 nothing is hipified and no JIT cache is used, so the built files travel with the
 source tree.
 
-Usage: ``python -m flash_attention_2_lab_amd._build``.
+Usage: ``python flash_attention_2_lab_amd/_build.py`` (run as a script: importing it
+through the package would need the libraries it builds).
 """
 
 from __future__ import annotations

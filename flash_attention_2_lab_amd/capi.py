@@ -25,6 +25,7 @@ FA2_STATUS_BAD_HEAD_DIM = 3
 FA2_STATUS_BAD_SEQUENCE_LENGTH = 4
 FA2_STATUS_MISALIGNED = 5
 FA2_STATUS_TOO_LARGE = 6
+FA2_STATUS_BAD_KEY_TILE = 7
 FA2_STATUS_HIP_ERROR_BASE = 1000
 
 
@@ -39,7 +40,7 @@ class Fa2Error(RuntimeError):
 def _load() -> ctypes.CDLL:
     if not LIBRARY_PATH.exists():
         raise ImportError(
-            f"{LIBRARY_PATH} is missing (run `python -m flash_attention_2_lab_amd._build`)"
+            f"{LIBRARY_PATH} is missing (run `python flash_attention_2_lab_amd/_build.py`)"
         )
     lib = ctypes.CDLL(str(LIBRARY_PATH))
     lib.fa2_forward_production_128x128.argtypes = [
@@ -48,6 +49,12 @@ def _load() -> ctypes.CDLL:
         ctypes.c_int, ctypes.c_void_p,
     ]
     lib.fa2_forward_production_128x128.restype = ctypes.c_int
+    lib.fa2_forward_tensorcore.argtypes = [
+        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+        ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+        ctypes.c_int64, ctypes.c_void_p,
+    ]
+    lib.fa2_forward_tensorcore.restype = ctypes.c_int
     lib.fa2_status_string.argtypes = [ctypes.c_int]
     lib.fa2_status_string.restype = ctypes.c_char_p
     lib.fa2_abi_version.argtypes = []
@@ -98,4 +105,32 @@ def forward_production_128x128(query: torch.Tensor, key: torch.Tensor, value: to
     )
     if status != FA2_STATUS_SUCCESS:
         raise Fa2Error("fa2_forward_production_128x128", status, status_string(status))
+    return output
+
+
+def forward_tensorcore_raw(query_ptr: int, key_ptr: int, value_ptr: int, output_ptr: int,
+                           batch: int, heads: int, seq_len: int, head_dim: int, key_tile: int,
+                           stream: int | None) -> int:
+    """Direct call of the noncausal C entry point; returns the status code."""
+    return lib.fa2_forward_tensorcore(
+        query_ptr, key_ptr, value_ptr, output_ptr, batch, heads, seq_len, head_dim, key_tile,
+        stream,
+    )
+
+
+def forward_tensorcore(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                       key_tile: int = 16, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """Allocate the output and run the noncausal entry (seq_len % key_tile == 0)."""
+    if query.dim() != 4:
+        raise ValueError("query must have shape [B, H, N, D]")
+    output = torch.empty_like(query)
+    if stream is None:
+        stream = torch.cuda.current_stream(query.device)
+    batch, heads, seq_len, head_dim = query.shape
+    status = forward_tensorcore_raw(
+        query.data_ptr(), key.data_ptr(), value.data_ptr(), output.data_ptr(),
+        batch, heads, seq_len, head_dim, key_tile, stream.cuda_stream,
+    )
+    if status != FA2_STATUS_SUCCESS:
+        raise Fa2Error("fa2_forward_tensorcore", status, status_string(status))
     return output

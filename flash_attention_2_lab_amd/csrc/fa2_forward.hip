@@ -526,6 +526,10 @@ void fa2_forward_d64_kernel(const _Float16* __restrict__ query,
 // adds no waits for them; the kernel waits with explicit vmcnt. M0 is a reserved
 // register that the compiler sets before each of its own uses, so listing it as
 // clobbered is only documentation (clang warns about reserved clobbers).
+//  - dma16_asm: tile offset in the scalar offset, for tiles inside the slab.
+//  - dma16_asm_checked: the whole byte offset in the VGPR offset, which the buffer
+//    unit checks against num_records (the scalar offset is not checked), so rows at
+//    or past seq_len read as zeros: used for a partial last key tile.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16_asm(u32x4 src, uint32_t lds_addr, int lane_offset,
@@ -533,6 +537,11 @@ __device__ __forceinline__ void dma16_asm(u32x4 src, uint32_t lds_addr, int lane
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                  :: "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(lane_offset), "s"(src),
                     "s"(__builtin_amdgcn_readfirstlane(src_offset))
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma16_asm_checked(u32x4 src, uint32_t lds_addr, int offset) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :: "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(offset), "s"(src)
                  : "memory", "m0");
 }
 #pragma clang diagnostic pop
@@ -554,13 +563,14 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
 }
 
 // Key-split variant for problems too small to fill the chip with 128-query
-// workgroups. A workgroup owns one 32-query block; its 4 waves each stream a
+// workgroups, and for sequence lengths that are not a multiple of 128 (any multiple
+// of 16: the last query block and the last key tile may be partial). A workgroup owns one 32-query block; its 4 waves each stream a
 // quarter of the key tiles that block sees, through two LDS stages of their own
 // (each wave fetches and reads only its own stages, so the key loop has no
 // workgroup barrier), and keep their own running max, sum and O. At the end the
 // four partial results are merged through LDS:
 //   m = max_w m_w,  l = sum_w l_w 2^((m_w - m) s log2e),  O = sum_w O_w 2^(...) / l.
-template <bool kCausal>
+template <bool kCausal, bool kPartial>
 __global__ __launch_bounds__(256) void fa2_forward_splitk_kernel(const _Float16* __restrict__ query,
                                                                  const _Float16* __restrict__ key,
                                                                  const _Float16* __restrict__ value,
@@ -598,8 +608,9 @@ __global__ __launch_bounds__(256) void fa2_forward_splitk_kernel(const _Float16*
 
     const int q0 = (int)qblock * kQueriesPerWave;
     const int my_query = q0 + lq;
+    const bool query_valid = !kPartial || my_query < seq_len;
     const int visible_tiles = kCausal ? (q0 + kQueriesPerWave - 1) / kKeysPerTile + 1
-                                      : seq_len / kKeysPerTile;
+                                      : (seq_len + kKeysPerTile - 1) / kKeysPerTile;
     const int t_begin = wave * visible_tiles / kSplit;
     const int t_end = (wave + 1) * visible_tiles / kSplit;
 
@@ -607,21 +618,26 @@ __global__ __launch_bounds__(256) void fa2_forward_splitk_kernel(const _Float16*
     const uint32_t my_stages_addr = lds_address(my_stages);
     const int dma_off[2] = {dma_lane_offset(lane, 0), dma_lane_offset(lane, 1)};
     auto dma_tile = [&](int t, int st) {
+        const bool partial = kPartial && (t + 1) * kKeysPerTile > seq_len;  // wave-uniform
 #pragma unroll
         for (int n = 0; n < kDmaPerTile; ++n) {
             const int m = n >> 3;
             const int r0 = (n & 7) * 8;
-            dma16_asm(m ? v_head : k_head,
-                      my_stages_addr + (uint32_t)(st * kStageBytes + m * kTileBytes + r0 * kRowBytes),
-                      dma_off[n & 1], t * kTileBytes + r0 * kRowBytes);
+            const uint32_t lds = my_stages_addr + (uint32_t)(st * kStageBytes + m * kTileBytes + r0 * kRowBytes);
+            const int src = t * kTileBytes + r0 * kRowBytes;
+            if (partial) dma16_asm_checked(m ? v_head : k_head, lds, dma_off[n & 1] + src);
+            else dma16_asm(m ? v_head : k_head, lds, dma_off[n & 1], src);
         }
     };
 
+    // Lanes past the last query (partial block) score a zero query; their output
+    // is not stored.
     f16x8 q_frag[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
-        q_frag[ks] = *reinterpret_cast<const f16x8*>(q_head + (size_t)my_query * kHeadDim +
-                                                      ks * 16 + half * 8);
+        q_frag[ks] = query_valid ? *reinterpret_cast<const f16x8*>(q_head + (size_t)my_query * kHeadDim +
+                                                                   ks * 16 + half * 8)
+                                 : f16x8{};
     if (t_begin < t_end) dma_tile(t_begin, 0);
 
     const int k_row = key_of_mfma_row(lq);
@@ -678,13 +694,17 @@ __global__ __launch_bounds__(256) void fa2_forward_splitk_kernel(const _Float16*
             for (int b = 0; b < 2; ++b)
                 sc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[b][ks], q_frag[ks], sc[b], 0, 0, 0);
 
-        if (kCausal && t * kKeysPerTile + kKeysPerTile - 1 > q0) {
+        // Causal mask on tiles reaching past the block's first query; keys at or
+        // past seq_len (zeros from the DMA) on a partial last tile.
+        const bool causal_tile = kCausal && t * kKeysPerTile + kKeysPerTile - 1 > q0;
+        if (causal_tile || (kPartial && (t + 1) * kKeysPerTile > seq_len)) {
 #pragma unroll
             for (int b = 0; b < 2; ++b)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const int key_index = t * kKeysPerTile + 32 * b + 16 * (i >> 3) + 8 * half + (i & 7);
-                    if (key_index > my_query) sc[b][i] = -INFINITY;
+                    if ((kCausal && key_index > my_query) || (kPartial && key_index >= seq_len))
+                        sc[b][i] = -INFINITY;
                 }
         }
 
@@ -768,6 +788,7 @@ __global__ __launch_bounds__(256) void fa2_forward_splitk_kernel(const _Float16*
         weight[w] = m_w == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_w - m_tot) * scale_log2);
         l_tot += red_l[w * 64 + lane] * weight[w];
     }
+    if (kPartial && !query_valid) return;
     const float inv_l = 1.0f / l_tot;
     _Float16* o_row = o_head + (size_t)my_query * kHeadDim;
 #pragma unroll
@@ -786,16 +807,24 @@ __global__ __launch_bounds__(256) void fa2_forward_splitk_kernel(const _Float16*
     }
 }
 
+// kPartial instantiations (seq_len not a multiple of the 64-key tile) carry the
+// bounds checks of a partial last query block and key tile; the others have none.
 template <bool kCausal>
 hipError_t launch_splitk(const void* q, const void* k, const void* v, void* o,
                          int64_t batch_heads, int64_t seq_len, float scale_log2,
                          hipStream_t stream) {
-    const int64_t query_blocks = seq_len / kQueriesPerWave;
-    hipLaunchKernelGGL((fa2_forward_splitk_kernel<kCausal>), dim3((unsigned)(batch_heads * query_blocks)),
-                       dim3(256), 0, stream,
-                       static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
-                       static_cast<const _Float16*>(v), static_cast<_Float16*>(o),
-                       (int)seq_len, (int)query_blocks, scale_log2);
+    const int64_t query_blocks = (seq_len + kQueriesPerWave - 1) / kQueriesPerWave;
+    const dim3 grid((unsigned)(batch_heads * query_blocks));
+    const auto* qh = static_cast<const _Float16*>(q);
+    const auto* kh = static_cast<const _Float16*>(k);
+    const auto* vh = static_cast<const _Float16*>(v);
+    auto* oh = static_cast<_Float16*>(o);
+    if (seq_len % kKeysPerTile != 0)
+        hipLaunchKernelGGL((fa2_forward_splitk_kernel<kCausal, true>), grid, dim3(256), 0, stream,
+                           qh, kh, vh, oh, (int)seq_len, (int)query_blocks, scale_log2);
+    else
+        hipLaunchKernelGGL((fa2_forward_splitk_kernel<kCausal, false>), grid, dim3(256), 0, stream,
+                           qh, kh, vh, oh, (int)seq_len, (int)query_blocks, scale_log2);
     return hipGetLastError();
 }
 
@@ -823,15 +852,17 @@ int choose_waves(int64_t batch_heads, int64_t seq_len) {
 
 bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) != 0; }
 
-}  // namespace
 
-extern "C" int fa2_forward_production_128x128(const void* query, const void* key,
-                                              const void* value, void* output, int64_t batch,
-                                              int64_t heads, int64_t seq_len, int64_t head_dim,
-                                              int causal, void* stream) {
+// Shared argument checks and dispatch of the C entry points. `multiple` is the
+// divisor seq_len must have; sequence lengths that are multiples of 128 run the
+// 128-query kernel when the problem fills the chip, everything else the key-split
+// kernel (which handles partial query blocks and key tiles).
+int forward(const void* query, const void* key, const void* value, void* output, int64_t batch,
+            int64_t heads, int64_t seq_len, int64_t head_dim, int64_t multiple, bool causal,
+            void* stream) {
     if (batch < 0 || heads < 0 || seq_len < 0 || head_dim < 0) return FA2_STATUS_NEGATIVE_DIMENSION;
     if (head_dim != kHeadDim) return FA2_STATUS_BAD_HEAD_DIM;
-    if (seq_len % kQueryTileAlign != 0) return FA2_STATUS_BAD_SEQUENCE_LENGTH;
+    if (seq_len % multiple != 0) return FA2_STATUS_BAD_SEQUENCE_LENGTH;
     if (batch == 0 || heads == 0 || seq_len == 0) return FA2_STATUS_SUCCESS;
     if (!query || !key || !value || !output) return FA2_STATUS_NULL_POINTER;
     if (misaligned(query) || misaligned(key) || misaligned(value) || misaligned(output))
@@ -841,14 +872,15 @@ extern "C" int fa2_forward_production_128x128(const void* query, const void* key
     if (seq_len > kMaxSeqLen || batch > (int64_t)UINT32_MAX / heads)
         return FA2_STATUS_TOO_LARGE;
     const int64_t batch_heads = batch * heads;
-    if (batch_heads > (int64_t)UINT32_MAX / (seq_len / kQueriesPerWave)) return FA2_STATUS_TOO_LARGE;
+    const int64_t query_blocks = (seq_len + kQueriesPerWave - 1) / kQueriesPerWave;
+    if (batch_heads > (int64_t)UINT32_MAX / query_blocks) return FA2_STATUS_TOO_LARGE;
 
     const float scale = 1.0f / sqrtf((float)kHeadDim);           // reference :3040-3046
     const float scale_log2 = scale * 1.4426950408889634074f;     // fold log2(e) for exp2
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const int waves = choose_waves(batch_heads, seq_len);
+    const bool full_tiles = seq_len % kQueryTileAlign == 0;
     hipError_t err;
-    if (waves == 4) {
+    if (full_tiles && choose_waves(batch_heads, seq_len) == 4) {
         err = causal ? launch_forward<true, 4>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
                      : launch_forward<false, 4>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
     } else {
@@ -858,15 +890,35 @@ extern "C" int fa2_forward_production_128x128(const void* query, const void* key
     return err == hipSuccess ? FA2_STATUS_SUCCESS : FA2_STATUS_HIP_ERROR_BASE + (int)err;
 }
 
+}  // namespace
+
+extern "C" int fa2_forward_production_128x128(const void* query, const void* key,
+                                              const void* value, void* output, int64_t batch,
+                                              int64_t heads, int64_t seq_len, int64_t head_dim,
+                                              int causal, void* stream) {
+    return forward(query, key, value, output, batch, heads, seq_len, head_dim, kQueryTileAlign,
+                   causal != 0, stream);
+}
+
+extern "C" int fa2_forward_tensorcore(const void* query, const void* key, const void* value,
+                                      void* output, int64_t batch, int64_t heads,
+                                      int64_t seq_len, int64_t head_dim, int64_t key_tile,
+                                      void* stream) {
+    if (key_tile != 16 && key_tile != 32) return FA2_STATUS_BAD_KEY_TILE;
+    return forward(query, key, value, output, batch, heads, seq_len, head_dim, key_tile,
+                   /*causal=*/false, stream);
+}
+
 extern "C" const char* fa2_status_string(int status) {
     switch (status) {
         case FA2_STATUS_SUCCESS: return "success";
         case FA2_STATUS_NULL_POINTER: return "null tensor pointer";
         case FA2_STATUS_NEGATIVE_DIMENSION: return "negative dimension";
         case FA2_STATUS_BAD_HEAD_DIM: return "head dimension must equal 64";
-        case FA2_STATUS_BAD_SEQUENCE_LENGTH: return "sequence length must be divisible by 128";
+        case FA2_STATUS_BAD_SEQUENCE_LENGTH: return "sequence length not a multiple of the entry's key tile";
         case FA2_STATUS_MISALIGNED: return "tensor pointer not 16-byte aligned";
         case FA2_STATUS_TOO_LARGE: return "problem too large for the kernel's launch grid";
+        case FA2_STATUS_BAD_KEY_TILE: return "key tile must be 16 or 32";
         default: break;
     }
     if (status > FA2_STATUS_HIP_ERROR_BASE)

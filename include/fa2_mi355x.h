@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define FA2_MI355X_ABI_VERSION 1
+#define FA2_MI355X_ABI_VERSION 2
 
 enum fa2_status {
     FA2_STATUS_SUCCESS = 0,
@@ -33,6 +33,7 @@ enum fa2_status {
     FA2_STATUS_BAD_SEQUENCE_LENGTH = 4, /* seq_len not a multiple of the entry's key tile    */
     FA2_STATUS_MISALIGNED = 5,          /* a tensor pointer is not 16-byte aligned           */
     FA2_STATUS_TOO_LARGE = 6,           /* seq_len > 2^24 or launch grid beyond 2^32 groups */
+    FA2_STATUS_BAD_KEY_TILE = 7,        /* fa2_forward_tensorcore: key_tile not 16 or 32     */
     FA2_STATUS_HIP_ERROR_BASE = 1000    /* + hipError_t from the launch                      */
 };
 
@@ -53,6 +54,24 @@ int fa2_forward_production_128x128(const void* query, const void* key, const voi
                                    void* output, int64_t batch, int64_t heads,
                                    int64_t seq_len, int64_t head_dim, int causal,
                                    void* stream);
+
+/*
+ * Noncausal fused attention forward for any seq_len that is a multiple of
+ * key_tile (16 or 32); the last query block and key tile may be partial. Same
+ * arithmetic and output contract as fa2_forward_production_128x128.
+ *
+ * Replaces the reference's Bc=16/Bc=32 tensor-core entry points, which differ
+ * only in the sequence-length divisor they accept:
+ *   tensorcore_attention_forward                    key_tile 16
+ *   tensorcore_attention_forward_bc32               key_tile 32
+ *   tensorcore_attention_forward_bc32_raw_pv        key_tile 32
+ *   tensorcore_attention_forward_bc32_raw_qk_raw_pv key_tile 32
+ *   (reference csrc/tensorcore_attention.cu:3131-3189, implementation 2826-2967,
+ *    validation 2731-2823; bindings csrc/bindings.cpp:39-61 and 113-134).
+ */
+int fa2_forward_tensorcore(const void* query, const void* key, const void* value,
+                           void* output, int64_t batch, int64_t heads, int64_t seq_len,
+                           int64_t head_dim, int64_t key_tile, void* stream);
 
 /* Human-readable name of a status code returned by this library (static storage). */
 const char* fa2_status_string(int status);

@@ -14,7 +14,8 @@ from flash_attention_2_lab_amd import capi
 
 def test_library_exports_every_declared_function():
     declared = capi.declared_functions()
-    assert {"fa2_forward_production_128x128", "fa2_status_string", "fa2_abi_version"} <= set(declared)
+    assert {"fa2_forward_production_128x128", "fa2_forward_tensorcore", "fa2_status_string",
+            "fa2_abi_version"} <= set(declared)
     lib = ctypes.CDLL(str(capi.LIBRARY_PATH))
     for name in declared:
         assert hasattr(lib, name), f"{name} declared in include/fa2_mi355x.h but not exported"
@@ -29,7 +30,8 @@ def test_abi_version_matches_header():
 def test_status_codes_match_header():
     text = capi.HEADER_PATH.read_text()
     for name in ("SUCCESS", "NULL_POINTER", "NEGATIVE_DIMENSION", "BAD_HEAD_DIM",
-                 "BAD_SEQUENCE_LENGTH", "MISALIGNED", "TOO_LARGE", "HIP_ERROR_BASE"):
+                 "BAD_SEQUENCE_LENGTH", "MISALIGNED", "TOO_LARGE", "BAD_KEY_TILE",
+                 "HIP_ERROR_BASE"):
         value = int(re.search(rf"FA2_STATUS_{name} = (\d+)", text).group(1))
         assert getattr(capi, f"FA2_STATUS_{name}") == value
 
@@ -37,7 +39,8 @@ def test_status_codes_match_header():
 @pytest.mark.parametrize("status, text", [
     (capi.FA2_STATUS_SUCCESS, "success"),
     (capi.FA2_STATUS_BAD_HEAD_DIM, "head dimension must equal 64"),
-    (capi.FA2_STATUS_BAD_SEQUENCE_LENGTH, "sequence length must be divisible by 128"),
+    (capi.FA2_STATUS_BAD_SEQUENCE_LENGTH, "sequence length not a multiple of the entry's key tile"),
+    (capi.FA2_STATUS_BAD_KEY_TILE, "key tile must be 16 or 32"),
     (capi.FA2_STATUS_NULL_POINTER, "null tensor pointer"),
     (capi.FA2_STATUS_MISALIGNED, "tensor pointer not 16-byte aligned"),
     (999, "unknown status"),
@@ -92,3 +95,32 @@ def test_rejects_problem_beyond_launch_grid():
     # Rejected on sizes alone; the (never dereferenced) pointers are aligned and non-null.
     assert _call(seq_len=1 << 31, ptrs=(4096,) * 4) == capi.FA2_STATUS_TOO_LARGE
     assert _call(batch=1 << 20, heads=1 << 20, ptrs=(4096,) * 4) == capi.FA2_STATUS_TOO_LARGE
+
+
+def _call_tc(batch=1, heads=1, seq_len=32, head_dim=64, key_tile=16, ptrs=(0, 0, 0, 0)):
+    q, k, v, o = ptrs
+    return capi.forward_tensorcore_raw(q, k, v, o, batch, heads, seq_len, head_dim, key_tile, None)
+
+
+@pytest.mark.parametrize("key_tile", [0, 8, 64, 128, -16])
+def test_tensorcore_entry_rejects_key_tiles_other_than_16_and_32(key_tile):
+    assert _call_tc(key_tile=key_tile) == capi.FA2_STATUS_BAD_KEY_TILE
+
+
+@pytest.mark.parametrize("key_tile, seq_len", [(16, 8), (16, 24), (16, 100), (32, 16), (32, 48), (32, 1040)])
+def test_tensorcore_entry_rejects_sequence_not_multiple_of_key_tile(key_tile, seq_len):
+    assert _call_tc(key_tile=key_tile, seq_len=seq_len) == capi.FA2_STATUS_BAD_SEQUENCE_LENGTH
+
+
+@pytest.mark.parametrize("key_tile, seq_len", [(16, 16), (16, 80), (32, 96), (32, 1056)])
+def test_tensorcore_entry_accepts_multiples_of_key_tile(key_tile, seq_len):
+    # Accepted shapes get as far as the pointer checks (nothing is launched).
+    assert _call_tc(key_tile=key_tile, seq_len=seq_len) == capi.FA2_STATUS_NULL_POINTER
+
+
+def test_tensorcore_entry_shares_the_other_checks():
+    assert _call_tc(head_dim=32) == capi.FA2_STATUS_BAD_HEAD_DIM
+    assert _call_tc(batch=-1) == capi.FA2_STATUS_NEGATIVE_DIMENSION
+    assert _call_tc(seq_len=0) == capi.FA2_STATUS_SUCCESS
+    assert _call_tc(ptrs=(4096, 4104, 4096, 4096)) == capi.FA2_STATUS_MISALIGNED
+    assert _call_tc(seq_len=1 << 30, ptrs=(4096,) * 4) == capi.FA2_STATUS_TOO_LARGE

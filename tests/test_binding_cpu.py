@@ -79,3 +79,45 @@ def test_reference_grid_limit_on_batch_times_heads():
 def test_valid_inputs_pass_validation():
     CHECK(_half(), _half(), _half(), False)
     CHECK(_half((0, 2, 128, 64)), _half((0, 2, 128, 64)), _half((0, 2, 128, 64)), False)
+
+
+TENSORCORE_ENTRIES = {
+    "tensorcore_attention_forward": 16,
+    "tensorcore_attention_forward_bc32": 32,
+    "tensorcore_attention_forward_bc32_raw_pv": 32,
+    "tensorcore_attention_forward_bc32_raw_qk_raw_pv": 32,
+}
+
+
+@pytest.mark.parametrize("name", sorted(TENSORCORE_ENTRIES))
+def test_module_exposes_the_bc16_bc32_entry_points(name):
+    # Reference csrc/bindings.cpp:113-134: three positional tensors, noncausal.
+    entry = getattr(flash_attention_cuda, name)
+    with pytest.raises(RuntimeError, match="query must be a CUDA tensor"):
+        entry(_half((1, 1, 32, 64)), _half((1, 1, 32, 64)), _half((1, 1, 32, 64)))
+
+
+@pytest.mark.parametrize("key_tile, seq_len", [(16, 8), (16, 40), (32, 48), (32, 80), (32, 1040)])
+def test_tensorcore_entries_require_a_multiple_of_their_key_tile(key_tile, seq_len):
+    # Reference csrc/tensorcore_attention.cu:2818-2822 and tests/test_tensorcore_attention.py:155-179.
+    x = _half((1, 1, seq_len, 64))
+    with pytest.raises(RuntimeError, match=f"sequence length must be divisible by {key_tile}"):
+        flash_attention_cuda._check_tensorcore_inputs(x, x, x, key_tile, False)
+
+
+@pytest.mark.parametrize("key_tile, seq_len", [(16, 16), (16, 80), (32, 96), (32, 512)])
+def test_tensorcore_entries_accept_partial_128_tiles(key_tile, seq_len):
+    x = _half((1, 1, seq_len, 64))
+    flash_attention_cuda._check_tensorcore_inputs(x, x, x, key_tile, False)
+
+
+def test_tensorcore_entries_share_the_reference_checks():
+    with pytest.raises(RuntimeError, match="head dimension must equal 64"):
+        x = _half((1, 1, 32, 16))
+        flash_attention_cuda._check_tensorcore_inputs(x, x, x, 16, False)
+    with pytest.raises(RuntimeError, match="query and key must have identical shapes"):
+        flash_attention_cuda._check_tensorcore_inputs(_half((1, 2, 32, 64)), _half((1, 1, 32, 64)),
+                                                      _half((1, 2, 32, 64)), 32, False)
+    x = torch.empty((65536, 1, 32, 64), dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="batch \\* heads exceeds CUDA grid.y limit"):
+        flash_attention_cuda._check_tensorcore_inputs(x, x, x, 32, False)

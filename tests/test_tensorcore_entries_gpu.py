@@ -1,0 +1,119 @@
+"""GPU tests of the Bc=16/32 tensor-core entry points (noncausal, N % 16 or N % 32).
+
+Reference: csrc/bindings.cpp:39-61, 113-134; csrc/tensorcore_attention.cu:2731-2967,
+3131-3189; tests/test_tensorcore_attention.py:15-299 (mirrored here at 3e-2 against an
+FP32 evaluation on the CPU). The oracle parity cases hold them to the north-star gate
+(atol 2e-3 + rtol 1e-2 against the FP32 oracle) on partial query blocks and key tiles.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import flash_attention_2_lab_amd as fa
+from flash_attention_2_lab_amd import capi
+from oracle import attention_reference_fp32
+
+pytestmark = pytest.mark.gpu
+
+MODULE = fa.flash_attention_cuda
+BC32_ENTRIES = ["tensorcore_attention_forward_bc32", "tensorcore_attention_forward_bc32_raw_pv",
+                "tensorcore_attention_forward_bc32_raw_qk_raw_pv"]
+
+
+def _inputs(batch, heads, seq_len, seed=0):
+    gen = torch.Generator().manual_seed(seed)
+    shape = (batch, heads, seq_len, 64)
+    return tuple(torch.randn(shape, generator=gen).half() for _ in range(3))
+
+
+@pytest.mark.parametrize("batch, heads, seq_len", [(1, 1, 16), (1, 2, 64), (1, 4, 80), (1, 8, 128), (2, 3, 256)])
+def test_bc16_matches_reference_formula(batch, heads, seq_len):
+    # Reference tests/test_tensorcore_attention.py:15-78.
+    torch.manual_seed(0)
+    query = torch.randn(batch, heads, seq_len, 64, device="cuda", dtype=torch.float16)
+    key = torch.randn_like(query)
+    value = torch.randn_like(query)
+    actual = MODULE.tensorcore_attention_forward(query, key, value)
+    q, k, v = (t.float().cpu() for t in (query, key, value))
+    expected = torch.softmax((q @ k.transpose(-2, -1)) / math.sqrt(64), dim=-1) @ v
+    assert actual.dtype == torch.float16
+    assert actual.shape == expected.shape
+    torch.testing.assert_close(actual.float().cpu(), expected, rtol=3e-2, atol=3e-2)
+
+
+@pytest.mark.parametrize("name", BC32_ENTRIES)
+@pytest.mark.parametrize("batch, heads, seq_len", [(1, 1, 32), (1, 2, 64), (1, 4, 96), (1, 8, 128), (1, 8, 512)])
+def test_bc32_entries_match_sdpa(name, batch, heads, seq_len):
+    # Reference tests/test_tensorcore_attention.py:81-152, 182-234, 240-299 (SDPA here
+    # on the CPU in FP32).
+    torch.manual_seed(0)
+    shape = (batch, heads, seq_len, 64)
+    query = torch.randn(shape, device="cuda", dtype=torch.float16)
+    key = torch.randn_like(query)
+    value = torch.randn_like(query)
+    expected = F.scaled_dot_product_attention(query.float().cpu(), key.float().cpu(),
+                                              value.float().cpu(), dropout_p=0.0,
+                                              is_causal=False).half()
+    actual = getattr(MODULE, name)(query, key, value)
+    assert actual.shape == expected.shape
+    torch.testing.assert_close(actual.cpu(), expected, rtol=3e-2, atol=3e-2)
+
+
+@pytest.mark.parametrize("name", BC32_ENTRIES)
+def test_bc32_entries_reject_partial_key_tile(name):
+    # Reference tests/test_tensorcore_attention.py:155-179.
+    x = torch.randn((1, 1, 48, 64), device="cuda", dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="divisible by 32"):
+        getattr(MODULE, name)(x, x, x)
+
+
+@pytest.mark.parametrize("batch, heads, seq_len", [
+    (1, 4, 16), (1, 4, 48), (1, 4, 80), (1, 4, 144), (2, 3, 208), (1, 8, 1040),
+    (1, 4, 320),     # multiple of 64, not of 128: key-split kernel without partial tiles
+    (4, 16, 2000),   # many workgroups, partial last tile
+    (2, 32, 1024),   # multiple of 128 that fills the chip: the 128-query kernel
+])
+def test_bc16_partial_tiles_match_oracle(batch, heads, seq_len):
+    q, k, v = _inputs(batch, heads, seq_len, seed=seq_len)
+    out = MODULE.tensorcore_attention_forward(q.cuda(), k.cuda(), v.cuda())
+    via_c_abi = capi.forward_tensorcore(q.cuda(), k.cuda(), v.cuda(), key_tile=16)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    torch.testing.assert_close(out.float().cpu(), attention_reference_fp32(q, k, v, causal=False),
+                               atol=2e-3, rtol=1e-2)
+    assert torch.equal(out, via_c_abi)
+
+
+def test_tensorcore_entries_agree_with_the_production_entry():
+    # Same kernels for a multiple of 128: bitwise equal outputs.
+    q, k, v = (t.cuda() for t in _inputs(1, 8, 512, seed=4))
+    production = MODULE.tensorcore_attention_forward_production_128x128(q, k, v, False)
+    for name in ["tensorcore_attention_forward"] + BC32_ENTRIES:
+        assert torch.equal(getattr(MODULE, name)(q, k, v), production), name
+
+
+def test_partial_tile_output_rows_past_the_end_are_not_written():
+    # The output buffer is exactly [B, H, N, 64]; guard rows beyond N by checking a
+    # padded allocation keeps its sentinel after the last head's rows.
+    q, k, v = (t.cuda() for t in _inputs(1, 2, 80, seed=5))
+    storage = torch.full((2 * 80 * 64 + 4096,), 7.0, device="cuda", dtype=torch.float16)
+    out = storage[: 2 * 80 * 64].view(1, 2, 80, 64)
+    status = capi.forward_tensorcore_raw(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                         1, 2, 80, 64, 16, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert status == capi.FA2_STATUS_SUCCESS
+    assert torch.all(storage[2 * 80 * 64:] == 7.0)
+    torch.testing.assert_close(out.float().cpu(), attention_reference_fp32(q.cpu(), k.cpu(), v.cpu(), causal=False),
+                               atol=2e-3, rtol=1e-2)
+
+
+def test_c_abi_rejects_bad_key_tile_on_device_pointers():
+    x = torch.zeros((1, 1, 32, 64), device="cuda", dtype=torch.float16)
+    status = capi.forward_tensorcore_raw(x.data_ptr(), x.data_ptr(), x.data_ptr(), x.data_ptr(),
+                                         1, 1, 32, 64, 64, None)
+    assert status == capi.FA2_STATUS_BAD_KEY_TILE

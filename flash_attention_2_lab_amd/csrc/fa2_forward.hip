@@ -319,12 +319,14 @@ void fa2_forward_d64_kernel(const _Float16* __restrict__ query,
     };
 
     // One exp pair: p = 2^(s*scale*log2e - m*scale*log2e) for accumulator registers
-    // 2q, 2q+1 of a block, rounded to FP16 (nearest) and added to the row sum
-    // (v_dot2_f32_f16 against 1.0, so the sum adds the FP16 values the MFMA uses).
+    // 2q, 2q+1 of a block, rounded to FP16 (nearest). Every second pair adds the
+    // last two pairs to the row sum: one packed FP16 add, then v_dot2_f32_f16
+    // against 1.0 into the FP32 sum (v_dot2 does not overlap MFMA execution,
+    // v_pk_add_f16 does, so this halves the dot2s at one extra FP16 rounding).
     auto exp_pair = [&](const f32x16& sb, int q, float m_scaled, f16x2 (&pk)[8], float& sum) {
         pk[q] = pack_rn(__builtin_amdgcn_exp2f(fmaf(sb[2 * q], scale_log2, -m_scaled)),
                         __builtin_amdgcn_exp2f(fmaf(sb[2 * q + 1], scale_log2, -m_scaled)));
-        sum = __builtin_amdgcn_fdot2(pk[q], ones, sum, false);
+        if (q & 1) sum = __builtin_amdgcn_fdot2(pk[q - 1] + pk[q], ones, sum, false);
     };
     // The 8 pairs of a block as the B operands of its two P.V MFMAs (16 keys each).
     auto assemble = [&](const f16x2 (&pk)[8], f16x8 (&p)[2]) {

@@ -566,23 +566,28 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
 
 // Key-split variant for problems too small to fill the chip with 128-query
 // workgroups, and for sequence lengths that are not a multiple of 128 (any multiple
-// of 16: the last query block and the last key tile may be partial). A workgroup owns one 32-query block; its 4 waves each stream a
-// quarter of the key tiles that block sees, through two LDS stages of their own
-// (each wave fetches and reads only its own stages, so the key loop has no
-// workgroup barrier), and keep their own running max, sum and O. At the end the
-// four partial results are merged through LDS:
+// of 16: the last query block and the last key tile may be partial). A workgroup
+// owns one 32-query block; its kSplit waves each stream a contiguous share of the
+// key tiles (kBlocks 32-key blocks each) that block sees, through two LDS stages
+// of their own (each wave fetches and reads only its own stages, so the key loop
+// has no workgroup barrier), and keep their own running max, sum and O. At the end
+// the partial results are merged through LDS:
 //   m = max_w m_w,  l = sum_w l_w 2^((m_w - m) s log2e),  O = sum_w O_w 2^(...) / l.
-template <bool kCausal, bool kPartial>
-__global__ __launch_bounds__(256) void fa2_forward_splitk_kernel(const _Float16* __restrict__ query,
+template <bool kCausal, bool kPartial, int kSplit, int kBlocks>
+__global__ __launch_bounds__(kSplit * 64) void fa2_forward_splitk_kernel(const _Float16* __restrict__ query,
                                                                  const _Float16* __restrict__ key,
                                                                  const _Float16* __restrict__ value,
                                                                  _Float16* __restrict__ output,
                                                                  int seq_len, int num_query_blocks,
                                                                  float scale_log2) {
-    constexpr int kSplit = 4;
-    constexpr int kStageBytes = 2 * kTileBytes;             // K tile then V tile
-    constexpr int kDmaPerTile = 2 * kTileBytes / 1024;      // one wave fetches whole tiles
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[kSplit * 2 * kStageBytes];
+    constexpr int kTileKeys = 32 * kBlocks;
+    constexpr int kTileBytesW = kTileKeys * kRowBytes;
+    constexpr int kStageBytes = 2 * kTileBytesW;            // K tile then V tile
+    constexpr int kDmaPerMatrix = kTileBytesW / 1024;        // 1 KiB = 8 rows per instruction
+    constexpr int kDmaPerTile = 2 * kDmaPerMatrix;           // one wave fetches whole tiles
+    constexpr int kMergeBytes = kSplit * (8 * 64 * 16 + 2 * 64 * 4);
+    constexpr int kSmemBytes = kSplit * 2 * kStageBytes > kMergeBytes ? kSplit * 2 * kStageBytes : kMergeBytes;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmemBytes];
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -611,8 +616,8 @@ __global__ __launch_bounds__(256) void fa2_forward_splitk_kernel(const _Float16*
     const int q0 = (int)qblock * kQueriesPerWave;
     const int my_query = q0 + lq;
     const bool query_valid = !kPartial || my_query < seq_len;
-    const int visible_tiles = kCausal ? (q0 + kQueriesPerWave - 1) / kKeysPerTile + 1
-                                      : (seq_len + kKeysPerTile - 1) / kKeysPerTile;
+    const int visible_tiles = kCausal ? (q0 + kQueriesPerWave - 1) / kTileKeys + 1
+                                      : (seq_len + kTileKeys - 1) / kTileKeys;
     const int t_begin = wave * visible_tiles / kSplit;
     const int t_end = (wave + 1) * visible_tiles / kSplit;
 
@@ -620,15 +625,16 @@ __global__ __launch_bounds__(256) void fa2_forward_splitk_kernel(const _Float16*
     const uint32_t my_stages_addr = lds_address(my_stages);
     const int dma_off[2] = {dma_lane_offset(lane, 0), dma_lane_offset(lane, 1)};
     auto dma_tile = [&](int t, int st) {
-        const bool partial = kPartial && (t + 1) * kKeysPerTile > seq_len;  // wave-uniform
+        const bool partial = kPartial && (t + 1) * kTileKeys > seq_len;  // wave-uniform
 #pragma unroll
         for (int n = 0; n < kDmaPerTile; ++n) {
-            const int m = n >> 3;
-            const int r0 = (n & 7) * 8;
-            const uint32_t lds = my_stages_addr + (uint32_t)(st * kStageBytes + m * kTileBytes + r0 * kRowBytes);
-            const int src = t * kTileBytes + r0 * kRowBytes;
-            if (partial) dma16_asm_checked(m ? v_head : k_head, lds, dma_off[n & 1] + src);
-            else dma16_asm(m ? v_head : k_head, lds, dma_off[n & 1], src);
+            const int m = n / kDmaPerMatrix;
+            const int r0 = (n % kDmaPerMatrix) * 8;
+            const uint32_t lds = my_stages_addr + (uint32_t)(st * kStageBytes + m * kTileBytesW + r0 * kRowBytes);
+            const int src = t * kTileBytesW + r0 * kRowBytes;
+            const int off = dma_off[(r0 >> 3) & 1];
+            if (partial) dma16_asm_checked(m ? v_head : k_head, lds, off + src);
+            else dma16_asm(m ? v_head : k_head, lds, off, src);
         }
     };
 
@@ -677,34 +683,34 @@ __global__ __launch_bounds__(256) void fa2_forward_splitk_kernel(const _Float16*
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         }
         const uint8_t* k_lds = my_stages + st * kStageBytes;
-        const uint8_t* v_lds = k_lds + kTileBytes;
+        const uint8_t* v_lds = k_lds + kTileBytesW;
 
-        // S^T = K Q^T for the tile's two 32-key blocks.
-        f16x8 kf[2][4];
+        // S^T = K Q^T for the tile's 32-key blocks.
+        f16x8 kf[kBlocks][4];
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-            for (int b = 0; b < 2; ++b)
+            for (int b = 0; b < kBlocks; ++b)
                 kf[b][ks] = *reinterpret_cast<const f16x8*>(k_lds + b * 32 * kRowBytes + k_off[ks]);
-        f32x16 sc[2];
+        f32x16 sc[kBlocks];
         const f32x16 zero = {};
 #pragma unroll
-        for (int b = 0; b < 2; ++b) sc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[b][0], q_frag[0], zero, 0, 0, 0);
+        for (int b = 0; b < kBlocks; ++b) sc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[b][0], q_frag[0], zero, 0, 0, 0);
 #pragma unroll
         for (int ks = 1; ks < 4; ++ks)
 #pragma unroll
-            for (int b = 0; b < 2; ++b)
+            for (int b = 0; b < kBlocks; ++b)
                 sc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[b][ks], q_frag[ks], sc[b], 0, 0, 0);
 
         // Causal mask on tiles reaching past the block's first query; keys at or
         // past seq_len (zeros from the DMA) on a partial last tile.
-        const bool causal_tile = kCausal && t * kKeysPerTile + kKeysPerTile - 1 > q0;
-        if (causal_tile || (kPartial && (t + 1) * kKeysPerTile > seq_len)) {
+        const bool causal_tile = kCausal && t * kTileKeys + kTileKeys - 1 > q0;
+        if (causal_tile || (kPartial && (t + 1) * kTileKeys > seq_len)) {
 #pragma unroll
-            for (int b = 0; b < 2; ++b)
+            for (int b = 0; b < kBlocks; ++b)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
-                    const int key_index = t * kKeysPerTile + 32 * b + 16 * (i >> 3) + 8 * half + (i & 7);
+                    const int key_index = t * kTileKeys + 32 * b + 16 * (i >> 3) + 8 * half + (i & 7);
                     if ((kCausal && key_index > my_query) || (kPartial && key_index >= seq_len))
                         sc[b][i] = -INFINITY;
                 }
@@ -713,7 +719,7 @@ __global__ __launch_bounds__(256) void fa2_forward_splitk_kernel(const _Float16*
         // Online softmax with the lazy rescale (bound 2^kRescaleLog2).
         float tile_max = -INFINITY;
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int b = 0; b < kBlocks; ++b)
 #pragma unroll
             for (int i = 0; i < 16; i += 2) tile_max = fmaxf(fmaxf(tile_max, sc[b][i]), sc[b][i + 1]);
         tile_max = max_across_halves(tile_max);
@@ -729,10 +735,10 @@ __global__ __launch_bounds__(256) void fa2_forward_splitk_kernel(const _Float16*
             m_run = m_new;
         }
         const float m_scaled = m_run * scale_log2;
-        f16x8 pf[2][2];
+        f16x8 pf[kBlocks][2];
         float sum0 = 0.0f, sum1 = 0.0f;
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
+        for (int b = 0; b < kBlocks; ++b) {
             f16x2 pk[8];
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
@@ -752,7 +758,7 @@ __global__ __launch_bounds__(256) void fa2_forward_splitk_kernel(const _Float16*
 
         // O^T += V^T P^T.
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
+        for (int k = 0; k < 4 * kBlocks; ++k) {
             const int row_base = (32 * (k >> 2) + 16 * ((k >> 1) & 1)) * kRowBytes;
             const f16x4 v_lo = lds_read_transposed(v_lds + row_base + v_off[0][k & 1]);
             const f16x4 v_hi = lds_read_transposed(v_lds + row_base + v_off[1][k & 1]);
@@ -761,7 +767,7 @@ __global__ __launch_bounds__(256) void fa2_forward_splitk_kernel(const _Float16*
         }
     }
 
-    // Merge the four partial results (stages are free once every wave is done).
+    // Merge the partial results (stages are free once every wave is done).
     __syncthreads();
     float* red_o = reinterpret_cast<float*>(smem);                  // [wave][8][64 lanes][4]
     float* red_m = red_o + kSplit * 8 * 64 * 4;                      // [wave][64]
@@ -776,7 +782,6 @@ __global__ __launch_bounds__(256) void fa2_forward_splitk_kernel(const _Float16*
     red_m[wave * 64 + lane] = m_run;
     red_l[wave * 64 + lane] = sum_across_halves(l_run);
     __syncthreads();
-    if (wave != 0) return;
 
     float m_tot = -INFINITY;
 #pragma unroll
@@ -793,8 +798,11 @@ __global__ __launch_bounds__(256) void fa2_forward_splitk_kernel(const _Float16*
     if (kPartial && !query_valid) return;
     const float inv_l = 1.0f / l_tot;
     _Float16* o_row = o_head + (size_t)my_query * kHeadDim;
+    // Wave w writes float groups j = w, w + kSplit, ... of the 8.
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j0 = 0; j0 < 8; j0 += kSplit) {
+        const int j = j0 + wave;
+        if (kSplit < 8 && j >= 8) break;
         f32x4 acc = {};
 #pragma unroll
         for (int w = 0; w < kSplit; ++w) {
@@ -811,22 +819,23 @@ __global__ __launch_bounds__(256) void fa2_forward_splitk_kernel(const _Float16*
 
 // kPartial instantiations (seq_len not a multiple of the 64-key tile) carry the
 // bounds checks of a partial last query block and key tile; the others have none.
-template <bool kCausal>
+template <bool kCausal, int kSplit, int kBlocks>
 hipError_t launch_splitk(const void* q, const void* k, const void* v, void* o,
                          int64_t batch_heads, int64_t seq_len, float scale_log2,
                          hipStream_t stream) {
     const int64_t query_blocks = (seq_len + kQueriesPerWave - 1) / kQueriesPerWave;
     const dim3 grid((unsigned)(batch_heads * query_blocks));
+    const dim3 block(kSplit * 64);
     const auto* qh = static_cast<const _Float16*>(q);
     const auto* kh = static_cast<const _Float16*>(k);
     const auto* vh = static_cast<const _Float16*>(v);
     auto* oh = static_cast<_Float16*>(o);
-    if (seq_len % kKeysPerTile != 0)
-        hipLaunchKernelGGL((fa2_forward_splitk_kernel<kCausal, true>), grid, dim3(256), 0, stream,
-                           qh, kh, vh, oh, (int)seq_len, (int)query_blocks, scale_log2);
+    if (seq_len % (32 * kBlocks) != 0)
+        hipLaunchKernelGGL((fa2_forward_splitk_kernel<kCausal, true, kSplit, kBlocks>), grid, block, 0,
+                           stream, qh, kh, vh, oh, (int)seq_len, (int)query_blocks, scale_log2);
     else
-        hipLaunchKernelGGL((fa2_forward_splitk_kernel<kCausal, false>), grid, dim3(256), 0, stream,
-                           qh, kh, vh, oh, (int)seq_len, (int)query_blocks, scale_log2);
+        hipLaunchKernelGGL((fa2_forward_splitk_kernel<kCausal, false, kSplit, kBlocks>), grid, block, 0,
+                           stream, qh, kh, vh, oh, (int)seq_len, (int)query_blocks, scale_log2);
     return hipGetLastError();
 }
 
@@ -847,10 +856,18 @@ hipError_t launch_forward(const void* q, const void* k, const void* v, void* o,
 
 // 128-query workgroups (4 waves) when they fill the chip (two per CU); otherwise
 // the key-split kernel (one 32-query block per workgroup, keys split over 4 waves).
-int choose_waves(int64_t batch_heads, int64_t seq_len) {
-    constexpr int64_t kTargetGroups = 512;  // 2 per CU on 256 CUs
-    return batch_heads * (seq_len / 128) >= kTargetGroups ? 4 : 1;
+// Kernel choice from measured crossovers on MI355X (B*H*N/128 = number of
+// 128-query groups): the 128-query kernel once there are at least two groups per CU
+// for causal problems (fewer leave CUs idle behind the longest causal groups) and
+// one per CU for noncausal ones; below that the key-split kernel, with 64-key tiles
+// while one workgroup per CU covers the grid (256 or fewer 32-query blocks) and
+// 32-key tiles (half the LDS, two workgroups per CU) beyond.
+bool use_128_query_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
+    const int64_t groups = batch_heads * (seq_len / 128);
+    return groups >= (causal ? 512 : 256);
 }
+
+constexpr int64_t kSplitWideMaxBlocks = 256;
 
 bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) != 0; }
 
@@ -882,12 +899,15 @@ int forward(const void* query, const void* key, const void* value, void* output,
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool full_tiles = seq_len % kQueryTileAlign == 0;
     hipError_t err;
-    if (full_tiles && choose_waves(batch_heads, seq_len) == 4) {
+    if (full_tiles && use_128_query_kernel(batch_heads, seq_len, causal)) {
         err = causal ? launch_forward<true, 4>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
                      : launch_forward<false, 4>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
+    } else if (batch_heads * query_blocks <= kSplitWideMaxBlocks) {
+        err = causal ? launch_splitk<true, 4, 2>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
+                     : launch_splitk<false, 4, 2>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
     } else {
-        err = causal ? launch_splitk<true>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
-                     : launch_splitk<false>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
+        err = causal ? launch_splitk<true, 4, 1>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
+                     : launch_splitk<false, 4, 1>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
     }
     return err == hipSuccess ? FA2_STATUS_SUCCESS : FA2_STATUS_HIP_ERROR_BASE + (int)err;
 }

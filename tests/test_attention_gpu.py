@@ -64,8 +64,9 @@ def test_configs_b1_h8_match_oracle(seq_len, causal):
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("shape", [(1, 64, 1024), (1, 32, 1024), (2, 16, 2048), (3, 5, 384)])
 def test_workgroup_shapes_match_oracle(shape, causal):
-    # (1,64,1024) and (2,16,2048) fill the chip (128-query kernel); the others run the
-    # key-split kernel. (3,5,384) has a batch*heads that is not a multiple of the 8-XCD remap.
+    # (1,64,1024) and (2,16,2048) run the 128-query kernel in both modes, (1,32,1024)
+    # noncausal only (causal: key-split with 32-key tiles); (3,5,384) runs the key-split
+    # kernel with 64-key tiles and has a batch*heads that is not a multiple of the 8-XCD remap.
     q, k, v = _inputs(*shape, seed=3)
     out = _run(q, k, v, causal)
     _assert_close_to_oracle(out, attention_reference_fp32(q, k, v, causal=causal))

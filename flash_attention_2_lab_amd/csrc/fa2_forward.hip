@@ -485,9 +485,10 @@ void fa2_forward_d64_kernel(const _Float16* __restrict__ query,
         __syncthreads();  // waits for every outstanding DMA
     };
 
-    // Steady iterations need tiles j, j+1 unmasked for wave 0 (the workgroup's first
-    // query) and tile j+3 present; they run in groups of four from j = 0 so that
-    // j % 4 (the stage) is known at compile time.
+    // Steady iterations need tiles j and j+1 unmasked for wave 0 (the workgroup's
+    // first query); they run from j = 0 in groups of four plus a remainder of up to
+    // three, so that j % 4 (the stage) is known at compile time. The last tile and
+    // the causal diagonal tiles take the generic iteration.
     const int first_masked_tile = kCausal ? q_block / kKeysPerTile : num_tiles;
     const int steady_end = max(0, min(first_masked_tile - 1, num_tiles - 3));
     using S0 = std::integral_constant<int, 0>;
@@ -501,7 +502,12 @@ void fa2_forward_d64_kernel(const _Float16* __restrict__ query,
         steady(j + 2, S2{}, s_a, s_b);
         steady(j + 3, S3{}, s_b, s_a);
     }
-    bool flipped = false;
+    const int rest = steady_end - j;  // 0..3
+    if (rest >= 1) steady(j, S0{}, s_a, s_b);
+    if (rest >= 2) steady(j + 1, S1{}, s_b, s_a);
+    if (rest >= 3) steady(j + 2, S2{}, s_a, s_b);
+    j += rest;
+    bool flipped = (rest & 1) != 0;
     for (; j < num_tiles; ++j) {
         if (flipped) generic(j, s_b, s_a);
         else generic(j, s_a, s_b);
@@ -674,6 +680,50 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_splitk_kernel(const _
     float l_run = 0.0f;
     const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
 
+    // Exact tile max and lazy rescale of l and O; returns whether the max moved.
+    auto exact_max_update = [&](const f32x16 (&s)[kBlocks]) -> bool {
+        float tile_max = -INFINITY;
+#pragma unroll
+        for (int b = 0; b < kBlocks; ++b)
+#pragma unroll
+            for (int i = 0; i < 16; i += 2) tile_max = fmaxf(fmaxf(tile_max, s[b][i]), s[b][i + 1]);
+        tile_max = max_across_halves(tile_max);
+        const bool grow = tile_max * scale_log2 > m_run * scale_log2 + kRescaleLog2;
+        if (__builtin_amdgcn_ballot_w64(grow) == 0) return false;
+        const float m_new = fmaxf(m_run, tile_max);
+        const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
+        l_run *= alpha;
+#pragma unroll
+        for (int d = 0; d < 2; ++d)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o_acc[d][i] *= alpha;
+        m_run = m_new;
+        return true;
+    };
+    // FP16 probabilities of a tile against the running max as P.V B operands; returns
+    // the lane sum (pairs added in FP16, then v_dot2 against 1.0 into FP32).
+    auto tile_probs = [&](const f32x16 (&s)[kBlocks], f16x8 (&pf)[kBlocks][2]) -> float {
+        const float m_scaled = m_run * scale_log2;
+        float sum = 0.0f;
+#pragma unroll
+        for (int b = 0; b < kBlocks; ++b) {
+            f16x2 pk[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                pk[q] = pack_rn(__builtin_amdgcn_exp2f(fmaf(s[b][2 * q], scale_log2, -m_scaled)),
+                                __builtin_amdgcn_exp2f(fmaf(s[b][2 * q + 1], scale_log2, -m_scaled)));
+                if (q & 1) sum = __builtin_amdgcn_fdot2(pk[q - 1] + pk[q], ones, sum, false);
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const f16x4 lo = __builtin_shufflevector(pk[4 * h], pk[4 * h + 1], 0, 1, 2, 3);
+                const f16x4 hi = __builtin_shufflevector(pk[4 * h + 2], pk[4 * h + 3], 0, 1, 2, 3);
+                pf[b][h] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            }
+        }
+        return sum;
+    };
+
     for (int t = t_begin; t < t_end; ++t) {
         const int st = (t - t_begin) & 1;
         if (t + 1 < t_end) {
@@ -716,45 +766,18 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_splitk_kernel(const _
                 }
         }
 
-        // Online softmax with the lazy rescale (bound 2^kRescaleLog2).
-        float tile_max = -INFINITY;
-#pragma unroll
-        for (int b = 0; b < kBlocks; ++b)
-#pragma unroll
-            for (int i = 0; i < 16; i += 2) tile_max = fmaxf(fmaxf(tile_max, sc[b][i]), sc[b][i + 1]);
-        tile_max = max_across_halves(tile_max);
-        const bool grow = tile_max * scale_log2 > m_run * scale_log2 + kRescaleLog2;
-        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-            const float m_new = fmaxf(m_run, tile_max);
-            const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
-            l_run *= alpha;
-#pragma unroll
-            for (int d = 0; d < 2; ++d)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) o_acc[d][i] *= alpha;
-            m_run = m_new;
-        }
-        const float m_scaled = m_run * scale_log2;
+        // Online softmax with the lazy rescale (bound 2^kRescaleLog2). The first tile
+        // of the wave takes the exact max; later tiles use the running max and check
+        // the lane sums (every probability is <= 2^8 when its lane's sum is), taking
+        // the exact max and recomputing only when a sum exceeds the bound.
         f16x8 pf[kBlocks][2];
-        float sum0 = 0.0f, sum1 = 0.0f;
-#pragma unroll
-        for (int b = 0; b < kBlocks; ++b) {
-            f16x2 pk[8];
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                pk[q] = pack_rn(__builtin_amdgcn_exp2f(fmaf(sc[b][2 * q], scale_log2, -m_scaled)),
-                                __builtin_amdgcn_exp2f(fmaf(sc[b][2 * q + 1], scale_log2, -m_scaled)));
-                if (q & 1) sum1 = __builtin_amdgcn_fdot2(pk[q], ones, sum1, false);
-                else sum0 = __builtin_amdgcn_fdot2(pk[q], ones, sum0, false);
-            }
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const f16x4 lo = __builtin_shufflevector(pk[4 * h], pk[4 * h + 1], 0, 1, 2, 3);
-                const f16x4 hi = __builtin_shufflevector(pk[4 * h + 2], pk[4 * h + 3], 0, 1, 2, 3);
-                pf[b][h] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-            }
+        const bool first = t == t_begin;
+        if (first) exact_max_update(sc);
+        float tile_sum = tile_probs(sc, pf);
+        if (!first && __builtin_amdgcn_ballot_w64(tile_sum > 256.0f) != 0) {
+            if (exact_max_update(sc)) tile_sum = tile_probs(sc, pf);
         }
-        l_run += sum0 + sum1;
+        l_run += tile_sum;
 
         // O^T += V^T P^T.
 #pragma unroll

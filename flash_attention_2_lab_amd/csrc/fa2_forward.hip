@@ -27,6 +27,10 @@
 //    while the softmax of tile j runs, so MFMA and VALU work overlap.
 //  * Causal mode stops the key loop at the diagonal, skips tiles a wave can never
 //    see and masks only diagonal tiles (key > query -> -inf).
+//  * Large problems run a wide variant with 64 queries per wave (two 32-query
+//    blocks sharing each K and V^T fragment), which halves the LDS traffic per
+//    FLOP: with random data the kernels run at the chip's power limit, and less
+//    data movement buys clock.
 //  * Workgroup ids are remapped so all query tiles of one (batch, head) land on the
 //    same XCD (dispatch is round-robin over the 8 XCDs), keeping that head's K/V
 //    resident in one L2; causal tiles run heaviest first.
@@ -840,6 +844,280 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_splitk_kernel(const _
     }
 }
 
+// Wide variant: 64 queries per wave, as two 32-query blocks (a: q_wave + 0..31,
+// b: q_wave + 32..63) that share every K and V^T fragment - each fragment read from
+// LDS feeds two MFMAs - so LDS reads and K/V fetches per FLOP are half those of the
+// 32-query kernel. With random data the chip runs at its power limit, and the
+// saved LDS traffic buys clock. Four waves (256 queries) per workgroup, two
+// workgroups per CU. A tile is three phases per wave (K reads and 16 score MFMAs;
+// V^T reads and the softmax of both blocks; 16 P.V MFMAs); the two waves of a
+// SIMD, from different workgroups, overlap one another's MFMA and softmax phases.
+// LDS: four 16 KiB stages (K then V), tile t in stage t % 4, fetched three tiles
+// ahead by LDS-DMA (inline assembly: the compiler adds no waits for it; the loop
+// waits with explicit vmcnt) with one barrier per tile.
+template <bool kCausal>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
+                                 const _Float16* __restrict__ key,
+                                 const _Float16* __restrict__ value,
+                                 _Float16* __restrict__ output,
+                                 int seq_len, int num_query_tiles, float scale_log2) {
+    constexpr int kWaves = 4;
+    constexpr int kWaveQueries = 2 * kQueriesPerWave;
+    constexpr int kBlockM = kWaves * kWaveQueries;
+    constexpr int kStages = 4;
+    constexpr int kStageBytes = 2 * kTileBytes;
+    constexpr int kDmaPerTile = kStageBytes / 1024 / kWaves;  // LDS-DMA instructions per wave
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kStageBytes];
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int lq = lane & 31;
+    const int half = lane >> 5;
+
+    // Workgroup -> (batch*head, query tile), XCD-contiguous; causal tiles run
+    // heaviest first.
+    const uint32_t groups = gridDim.x;
+    const uint32_t xcd = blockIdx.x & 7u;
+    const uint32_t slot = blockIdx.x >> 3;
+    const uint32_t per_xcd = groups >> 3;
+    const uint32_t extra = groups & 7u;
+    const uint32_t logical = xcd * per_xcd + min(xcd, extra) + slot;
+    const uint32_t bh = logical / (uint32_t)num_query_tiles;
+    uint32_t qtile = logical - bh * (uint32_t)num_query_tiles;
+    if (kCausal) qtile = (uint32_t)num_query_tiles - 1u - qtile;
+
+    const size_t head_offset = (size_t)bh * (size_t)seq_len * kHeadDim;
+    const _Float16* __restrict__ q_head = query + head_offset;
+    const u32x4 k_head = head_descriptor(key + head_offset, seq_len);
+    const u32x4 v_head = head_descriptor(value + head_offset, seq_len);
+    _Float16* __restrict__ o_head = output + head_offset;
+
+    const int q_block = (int)qtile * kBlockM;
+    const int q_wave = q_block + wave * kWaveQueries;
+    const int query_a = q_wave + lq;
+    const int query_b = query_a + kQueriesPerWave;
+    const int num_tiles = kCausal ? (q_block + kBlockM - 1) / kKeysPerTile + 1 : seq_len / kKeysPerTile;
+    // Causal: the wave's last tile is its diagonal tile (q_wave is a multiple of 64).
+    const int wave_last_tile = kCausal ? q_wave / kKeysPerTile : num_tiles - 1;
+
+    // Q^T fragments of both blocks (B operands of K Q^T).
+    f16x8 qa[4], qb[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        qa[ks] = *reinterpret_cast<const f16x8*>(q_head + (size_t)query_a * kHeadDim + ks * 16 + half * 8);
+        qb[ks] = *reinterpret_cast<const f16x8*>(q_head + (size_t)query_b * kHeadDim + ks * 16 + half * 8);
+    }
+
+    const uint32_t smem_addr = lds_address(smem);
+    const int dma_off[2] = {dma_lane_offset(lane, 0), dma_lane_offset(lane, 1)};
+    // This wave issues instructions n = wave + x * kWaves of a tile's 16 (8 per
+    // matrix, 8 rows each).
+    auto dma_tile = [&](int t) {
+        const uint32_t stage = smem_addr + (uint32_t)((t & (kStages - 1)) * kStageBytes);
+#pragma unroll
+        for (int x = 0; x < kDmaPerTile; ++x) {
+            const int n = wave + x * kWaves;
+            const int m = n >> 3;
+            const int r0 = (n & 7) * 8;
+            dma16_asm(m ? v_head : k_head, stage + (uint32_t)(m * kTileBytes + r0 * kRowBytes), dma_off[n & 1],
+                      t * kTileBytes + r0 * kRowBytes);
+        }
+    };
+    dma_tile(0);
+    if (num_tiles > 1) dma_tile(1);
+    if (num_tiles > 2) dma_tile(2);
+
+    const int k_row = key_of_mfma_row(lq);
+    const int k_swz = tile_swizzle(k_row);
+    int k_off[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) k_off[ks] = k_row * kRowBytes + (((2 * ks + half) ^ k_swz) << 4);
+    const int grp = lane >> 4;
+    const int i16 = lane & 15;
+    int v_off[2][2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int dblk = 0; dblk < 2; ++dblk) {
+            const int row = 8 * half + 4 * r + (i16 >> 2);
+            const int chunk = 4 * dblk + 2 * (grp & 1) + ((i16 & 3) >> 1);
+            v_off[r][dblk] = row * kRowBytes + ((chunk ^ tile_swizzle(row)) << 4) + 8 * (i16 & 1);
+        }
+
+    f32x16 oa[2], ob[2];
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            oa[d][i] = 0.0f;
+            ob[d][i] = 0.0f;
+        }
+    float m_a = -INFINITY, m_b = -INFINITY;  // running max of raw scores per block
+    float l_a = 0.0f, l_b = 0.0f;            // this lane's share of each denominator
+    const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+
+    // Exact tile max of one block and lazy rescale of its l and O (bound
+    // 2^kRescaleLog2); returns whether the max moved.
+    auto exact_max_update = [&](const f32x16 (&s)[2], float& m_run, float& l_run, f32x16 (&o)[2]) -> bool {
+        float tile_max = -INFINITY;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int i = 0; i < 16; i += 2) tile_max = fmaxf(fmaxf(tile_max, s[b][i]), s[b][i + 1]);
+        tile_max = max_across_halves(tile_max);
+        const bool grow = tile_max * scale_log2 > m_run * scale_log2 + kRescaleLog2;
+        if (__builtin_amdgcn_ballot_w64(grow) == 0) return false;
+        const float m_new = fmaxf(m_run, tile_max);
+        const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
+        l_run *= alpha;
+#pragma unroll
+        for (int d = 0; d < 2; ++d)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[d][i] *= alpha;
+        m_run = m_new;
+        return true;
+    };
+    // FP16 probabilities of one block against its running max, as P.V B operands
+    // (pf[key block][16-key half]); returns the lane sum (pairs added in FP16, then
+    // v_dot2 against 1.0 into FP32).
+    auto tile_probs = [&](const f32x16 (&s)[2], float m_run, f16x8 (&pf)[2][2]) -> float {
+        const float m_scaled = m_run * scale_log2;
+        float sum = 0.0f;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            f16x2 pk[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                pk[q] = pack_rn(__builtin_amdgcn_exp2f(fmaf(s[b][2 * q], scale_log2, -m_scaled)),
+                                __builtin_amdgcn_exp2f(fmaf(s[b][2 * q + 1], scale_log2, -m_scaled)));
+                if (q & 1) sum = __builtin_amdgcn_fdot2(pk[q - 1] + pk[q], ones, sum, false);
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const f16x4 lo = __builtin_shufflevector(pk[4 * h], pk[4 * h + 1], 0, 1, 2, 3);
+                const f16x4 hi = __builtin_shufflevector(pk[4 * h + 2], pk[4 * h + 3], 0, 1, 2, 3);
+                pf[b][h] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            }
+        }
+        return sum;
+    };
+
+    // Prologue: tiles 0..2 and Q landed. The empty asm consumes Q where the compiler
+    // adds its own wait for the Q loads: already satisfied here, whereas at the first
+    // MFMA its count would also cover the tile-3 fetch issued in between.
+    wait_dma_and_barrier<0>();
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) asm volatile("" ::"v"(qa[ks]), "v"(qb[ks]));
+
+    for (int t = 0; t < num_tiles; ++t) {
+        if (t + 3 < num_tiles) dma_tile(t + 3);  // into the stage tile t-1 used
+        if (t <= wave_last_tile) {
+            const uint8_t* k_lds = smem + (t & (kStages - 1)) * kStageBytes;
+            const uint8_t* v_lds = k_lds + kTileBytes;
+
+            // S^T = K Q^T of both blocks; each K fragment feeds two MFMAs. The MFMA
+            // phases run at raised wave priority: when both waves of a SIMD can
+            // issue, the one with MFMAs goes first and the other's softmax fills the
+            // MFMA shadow.
+            __builtin_amdgcn_s_setprio(1);
+            f16x8 kf[2][4];
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+                    kf[b][ks] = *reinterpret_cast<const f16x8*>(k_lds + b * 32 * kRowBytes + k_off[ks]);
+            f32x16 sa[2], sb[2];
+            const f32x16 zero = {};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
+                    sa[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[b][ks], qa[ks], ks == 0 ? zero : sa[b], 0, 0, 0);
+                    sb[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[b][ks], qb[ks], ks == 0 ? zero : sb[b], 0, 0, 0);
+                }
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_setprio(0);
+            // V^T fragments of the tile (P.V MFMA k: key block k/4, 16-key half
+            // (k/2)%2, d-block k%2), read while the softmax runs.
+            f16x8 vf[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int row_base = (32 * (k >> 2) + 16 * ((k >> 1) & 1)) * kRowBytes;
+                const f16x4 v_lo = lds_read_transposed(v_lds + row_base + v_off[0][k & 1]);
+                const f16x4 v_hi = lds_read_transposed(v_lds + row_base + v_off[1][k & 1]);
+                vf[k] = __builtin_shufflevector(v_lo, v_hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            }
+
+            // Causal mask on the wave's diagonal tile (keys 64t.. = q_wave..): register
+            // i of block b holds key 64t + 32b + 16(i/8) + 8*half + i%8.
+            if (kCausal && t == wave_last_tile) {
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int key_index = t * kKeysPerTile + 32 * b + 16 * (i >> 3) + 8 * half + (i & 7);
+                        if (key_index > query_a) sa[b][i] = -INFINITY;
+                        if (key_index > query_b) sb[b][i] = -INFINITY;
+                    }
+            }
+
+            // Online softmax per block: exact max on the first tile, then the running
+            // max with the lane-sum check (every probability is <= 2^8 when its lane's
+            // sum is), recomputing only a block whose check fails.
+            f16x8 pa[2][2], pb[2][2];
+            if (t == 0) {
+                exact_max_update(sa, m_a, l_a, oa);
+                exact_max_update(sb, m_b, l_b, ob);
+            }
+            float sum_a = tile_probs(sa, m_a, pa);
+            float sum_b = tile_probs(sb, m_b, pb);
+            if (t != 0) {
+                if (__builtin_amdgcn_ballot_w64(sum_a > 256.0f) != 0 && exact_max_update(sa, m_a, l_a, oa))
+                    sum_a = tile_probs(sa, m_a, pa);
+                if (__builtin_amdgcn_ballot_w64(sum_b > 256.0f) != 0 && exact_max_update(sb, m_b, l_b, ob))
+                    sum_b = tile_probs(sb, m_b, pb);
+            }
+            l_a += sum_a;
+            l_b += sum_b;
+
+            // O^T += V^T P^T for both blocks; each V^T fragment feeds two MFMAs.
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                oa[k & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[k], pa[k >> 2][(k >> 1) & 1], oa[k & 1], 0, 0, 0);
+                ob[k & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[k], pb[k >> 2][(k >> 1) & 1], ob[k & 1], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_setprio(0);
+        }
+        // Tile t+1 must have landed; only the fetches of the tiles after it may stay
+        // in flight. After the barrier every wave is done with tile t's stage.
+        if (t + 3 < num_tiles) wait_dma_and_barrier<2 * kDmaPerTile>();
+        else if (t + 2 < num_tiles) wait_dma_and_barrier<kDmaPerTile>();
+        else wait_dma_and_barrier<0>();
+    }
+
+    // Epilogue: O = O^T / l. Accumulator i of d-block dblk holds dim
+    // 32*dblk + 8*(i/4) + 4*half + i%4 of the lane's query.
+    auto store = [&](const f32x16 (&o)[2], float l_run, int q) {
+        const float inv_l = 1.0f / sum_across_halves(l_run);
+        _Float16* o_row = o_head + (size_t)q * kHeadDim;
+#pragma unroll
+        for (int dblk = 0; dblk < 2; ++dblk)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f16x2 a = pack_rn(o[dblk][4 * g + 0] * inv_l, o[dblk][4 * g + 1] * inv_l);
+                const f16x2 c = pack_rn(o[dblk][4 * g + 2] * inv_l, o[dblk][4 * g + 3] * inv_l);
+                *reinterpret_cast<f16x4*>(o_row + 32 * dblk + 8 * g + 4 * half) = __builtin_shufflevector(a, c, 0, 1, 2, 3);
+            }
+    };
+    store(oa, l_a, query_a);
+    store(ob, l_b, query_b);
+}
+
 // kPartial instantiations (seq_len not a multiple of the 64-key tile) carry the
 // bounds checks of a partial last query block and key tile; the others have none.
 template <bool kCausal, int kSplit, int kBlocks>
@@ -877,6 +1155,29 @@ hipError_t launch_forward(const void* q, const void* k, const void* v, void* o,
     return hipGetLastError();
 }
 
+template <bool kCausal>
+hipError_t launch_wide(const void* q, const void* k, const void* v, void* o, int64_t batch_heads,
+                       int64_t seq_len, float scale_log2, hipStream_t stream) {
+    const int64_t query_tiles = seq_len / 256;
+    hipLaunchKernelGGL((fa2_forward_d64_wide_kernel<kCausal>), dim3((unsigned)(batch_heads * query_tiles)),
+                       dim3(256), 0, stream, static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
+                       static_cast<const _Float16*>(v), static_cast<_Float16*>(o), (int)seq_len,
+                       (int)query_tiles, scale_log2);
+    return hipGetLastError();
+}
+
+// 256-query workgroups (64 queries per wave) once they fill every workgroup slot
+// of the chip (two per CU) for noncausal problems - below that the 128-query
+// kernel is faster - and from 2048 groups for causal ones, where the waves of a
+// 256-query group idle through up to three diagonal tiles: measured on MI355X,
+// B2 H32 N16384 causal runs 7% faster wide, B16 H16 N4096 causal the same, and
+// B1 H64 N4096 causal 13% slower.
+bool use_wide_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
+    if (seq_len % 256 != 0) return false;
+    const int64_t groups = batch_heads * (seq_len / 256);
+    return groups >= (causal ? 2048 : 512);
+}
+
 // 128-query workgroups (4 waves) when they fill the chip (two per CU); otherwise
 // the key-split kernel (one 32-query block per workgroup, keys split over 4 waves).
 // Kernel choice from measured crossovers on MI355X (B*H*N/128 = number of
@@ -896,9 +1197,9 @@ bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) !
 
 
 // Shared argument checks and dispatch of the C entry points. `multiple` is the
-// divisor seq_len must have; sequence lengths that are multiples of 128 run the
-// 128-query kernel when the problem fills the chip, everything else the key-split
-// kernel (which handles partial query blocks and key tiles).
+// divisor seq_len must have; sequence lengths that are multiples of 256 or 128 run
+// the 256- or 128-query kernel when the problem fills the chip, everything else the
+// key-split kernel (which handles partial query blocks and key tiles).
 int forward(const void* query, const void* key, const void* value, void* output, int64_t batch,
             int64_t heads, int64_t seq_len, int64_t head_dim, int64_t multiple, bool causal,
             void* stream) {
@@ -922,7 +1223,10 @@ int forward(const void* query, const void* key, const void* value, void* output,
     hipStream_t s = static_cast<hipStream_t>(stream);
     const bool full_tiles = seq_len % kQueryTileAlign == 0;
     hipError_t err;
-    if (full_tiles && use_128_query_kernel(batch_heads, seq_len, causal)) {
+    if (use_wide_kernel(batch_heads, seq_len, causal)) {
+        err = causal ? launch_wide<true>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
+                     : launch_wide<false>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
+    } else if (full_tiles && use_128_query_kernel(batch_heads, seq_len, causal)) {
         err = causal ? launch_forward<true, 4>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
                      : launch_forward<false, 4>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
     } else if (batch_heads * query_blocks <= kSplitWideMaxBlocks) {

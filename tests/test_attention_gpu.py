@@ -162,6 +162,26 @@ def test_growing_scores_match_oracle(shape, causal):
     _assert_close_to_oracle(out, attention_reference_fp32(q, k, v, causal=causal))
 
 
+@pytest.mark.parametrize("ramp", [False, True])
+@pytest.mark.parametrize("causal, shape", [(False, (8, 16, 1024)), (True, (8, 64, 1024))])
+def test_wide_workgroup_shapes_match_oracle(causal, shape, ramp):
+    # Large enough for the 256-query kernel (64 queries per wave as two 32-query
+    # blocks): every row of three whole heads - all four waves, both blocks of each
+    # wave and, causal, every diagonal tile - plus sampled rows of the others. With
+    # `ramp` the key norms grow 5x along the sequence, forcing the recompute path.
+    batch, heads, seq_len = shape
+    q, k, v = _inputs(*shape, seed=13)
+    if ramp:
+        k = (k.float() * torch.linspace(1.0, 5.0, seq_len).view(1, 1, -1, 1)).half()
+    out = _run(q, k, v, causal).cpu()
+    assert torch.isfinite(out).all()
+    whole = [(0, 0), (batch - 1, heads - 1), (batch // 2, heads // 3)]
+    rows = [(b, h, i) for b, h in whole for i in range(seq_len)] + _sample_rows(batch, heads, seq_len, 64, seed=14)
+    expected = attention_rows_fp32(q, k, v, rows, causal=causal)
+    actual = torch.stack([out[b, h, i] for b, h, i in rows])
+    _assert_close_to_oracle(actual, expected)
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_constant_value_gives_constant_output(causal):
     q, k, _ = _inputs(2, 4, 512, seed=5)

@@ -2,8 +2,9 @@
 
 Two shared objects are produced next to this file:
 
-* ``libfa2_mi355x.so`` - the HIP kernels and the C ABI of ``include/fa2_mi355x.h``,
-  compiled by hipcc for gfx950 only.
+* ``libfa2_mi355x.so`` - the HIP kernels and the C ABI of ``include/fa2_mi355x.h``
+  (``csrc/fa2_forward.hip``: the FP16 attention forward; ``csrc/fa2_aux.hip``: the
+  module's other operators), compiled by hipcc for gfx950 only.
 * ``flash_attention_cuda<EXT_SUFFIX>`` - the PyTorch operator module with the
   reference's entry-point names, compiled as host C++ against torch's headers and
   linked to ``libfa2_mi355x.so`` through an ``$ORIGIN`` rpath.
@@ -68,9 +69,12 @@ def _run(cmd: list[str]) -> None:
         print("\n".join(lines), file=sys.stderr)
 
 
+KERNEL_SOURCES = ("fa2_forward.hip", "fa2_aux.hip")
+
+
 def kernel_library_command() -> list[str]:
     return [HIPCC, *HIP_FLAGS, "-shared", f"-I{INCLUDE}",
-            str(CSRC / "fa2_forward.hip"), "-o", str(KERNEL_LIBRARY)]
+            *(str(CSRC / name) for name in KERNEL_SOURCES), "-o", str(KERNEL_LIBRARY)]
 
 
 def _extension_flags() -> tuple[list[str], list[str]]:

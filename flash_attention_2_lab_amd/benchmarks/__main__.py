@@ -15,7 +15,7 @@ import sys
 import torch
 
 from .harness import BenchmarkConfig, benchmark_operation
-from .kernels import KERNELS, NOT_BUILT
+from .kernels import KERNELS
 from .workloads import AttentionWorkload, attention_flops, generate_attention_inputs
 
 DTYPES: dict[str, torch.dtype] = {
@@ -62,14 +62,11 @@ def main(argv: list[str] | None = None) -> int:
     print(f"GPU:      {torch.cuda.get_device_name()}")
     print(f"Workload: {workload.label}")
     print()
-    unknown = set(args.kernels or ()) - {spec.name for spec in KERNELS} - set(NOT_BUILT)
+    unknown = set(args.kernels or ()) - {spec.name for spec in KERNELS}
     if unknown:
         print(f"unknown kernels: {', '.join(sorted(unknown))}", file=sys.stderr)
         return 2
     results = []
-    for name in NOT_BUILT:
-        if args.kernels is None or name in args.kernels:
-            print(f"{name:30s} not built (FP32 SIMT kernel of the reference)")
     for spec in KERNELS:
         if args.kernels is not None and spec.name not in args.kernels:
             continue

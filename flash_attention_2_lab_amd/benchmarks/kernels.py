@@ -2,11 +2,10 @@
 benchmarks/kernels.py:15-240).
 
 Each spec names a callable of (inputs, workload) and the workloads it supports. The
-tensor-core entries and their support predicates are the reference's, served by
-this library's HIP kernels; `pytorch_sdpa` is the device comparator and
-`pytorch_sdpa_cpu` an FP32 CPU comparator (torch's library routine on host copies
-of the inputs). The reference's FP32 SIMT kernels (naive_online, block_online,
-tiled_simt, tilewise_simt) are not part of this build.
+kernel names and support predicates are the reference's, served by this library's
+HIP kernels (the four FP32 SIMT names share one FP32 kernel); `pytorch_sdpa` is the
+device comparator and `pytorch_sdpa_cpu` an FP32 CPU comparator (torch's library
+routine on host copies of the inputs).
 """
 
 from __future__ import annotations
@@ -34,7 +33,7 @@ def _module():
     return flash_attention_2_lab_amd.flash_attention_cuda
 
 
-def _tensorcore(entry: str) -> Callable[[AttentionInputs, AttentionWorkload], torch.Tensor]:
+def _entry(entry: str) -> Callable[[AttentionInputs, AttentionWorkload], torch.Tensor]:
     def run(inputs: AttentionInputs, workload: AttentionWorkload) -> torch.Tensor:
         return getattr(_module(), entry)(inputs.query, inputs.key, inputs.value)
     run.__name__ = entry
@@ -54,6 +53,12 @@ def _sdpa(inputs: AttentionInputs, workload: AttentionWorkload) -> torch.Tensor:
 def _square_fp16_d64(workload: AttentionWorkload) -> bool:
     return (workload.dtype == torch.float16 and workload.query_length == workload.key_length
             and workload.head_dimension == 64)
+
+
+def _simt_support(head_dims: tuple[int, ...]) -> Callable[[AttentionWorkload], bool]:
+    # reference benchmarks/kernels.py:137-183
+    return lambda w: (w.dtype == torch.float32 and w.query_length == w.key_length
+                      and w.head_dimension in head_dims and not w.causal)
 
 
 def _tensorcore_support(multiple: int) -> Callable[[AttentionWorkload], bool]:
@@ -77,24 +82,25 @@ class _CpuSdpa:
 
 
 KERNELS: list[KernelSpec] = [
+    KernelSpec("naive_online", _entry("naive_attention_forward"), _simt_support((64, 128))),
     # bfloat16 SDPA on the device is left out: torch's bf16 batched products with a
     # transposed operand have faulted the GPU on this image.
     KernelSpec("pytorch_sdpa", _sdpa, lambda w: w.dtype in (torch.float16, torch.float32)),
-    KernelSpec("tensorcore_attention", _tensorcore("tensorcore_attention_forward"),
+    KernelSpec("block_online", _entry("block_attention_forward"), _simt_support((64, 128))),
+    KernelSpec("tiled_simt", _entry("tiled_attention_forward"), _simt_support((64,))),
+    KernelSpec("tilewise_simt", _entry("tilewise_attention_forward"), _simt_support((64,))),
+    KernelSpec("tensorcore_attention", _entry("tensorcore_attention_forward"),
                _tensorcore_support(16)),
-    KernelSpec("tensorcore_attention_bc32", _tensorcore("tensorcore_attention_forward_bc32"),
+    KernelSpec("tensorcore_attention_bc32", _entry("tensorcore_attention_forward_bc32"),
                _tensorcore_support(32)),
-    KernelSpec("tensorcore_bc32_raw_pv", _tensorcore("tensorcore_attention_forward_bc32_raw_pv"),
+    KernelSpec("tensorcore_bc32_raw_pv", _entry("tensorcore_attention_forward_bc32_raw_pv"),
                _tensorcore_support(32)),
     KernelSpec("tensorcore_bc32_raw_qk_raw_pv",
-               _tensorcore("tensorcore_attention_forward_bc32_raw_qk_raw_pv"), _tensorcore_support(32)),
+               _entry("tensorcore_attention_forward_bc32_raw_qk_raw_pv"), _tensorcore_support(32)),
     KernelSpec("tensorcore_production_128x128", _production,
                lambda w: _square_fp16_d64(w) and w.query_length % 128 == 0),
     KernelSpec("pytorch_sdpa_cpu", _CpuSdpa(), lambda w: True, on_device=False),
 ]
-
-# Names of the reference's kernels that this build does not provide.
-NOT_BUILT = ("naive_online", "block_online", "tiled_simt", "tilewise_simt")
 
 
 def find_kernel(name: str) -> KernelSpec:

@@ -55,6 +55,22 @@ def _load() -> ctypes.CDLL:
         ctypes.c_int64, ctypes.c_void_p,
     ]
     lib.fa2_forward_tensorcore.restype = ctypes.c_int
+    lib.fa2_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    lib.fa2_copy.restype = ctypes.c_int
+    lib.fa2_attention_scores_f32.argtypes = [
+        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+        ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+    ]
+    lib.fa2_attention_scores_f32.restype = ctypes.c_int
+    lib.fa2_attention_forward_f32.argtypes = [
+        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+        ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+    ]
+    lib.fa2_attention_forward_f32.restype = ctypes.c_int
+    lib.fa2_matmul_16x64x16_f16.argtypes = [
+        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+    ]
+    lib.fa2_matmul_16x64x16_f16.restype = ctypes.c_int
     lib.fa2_status_string.argtypes = [ctypes.c_int]
     lib.fa2_status_string.restype = ctypes.c_char_p
     lib.fa2_abi_version.argtypes = []
@@ -134,3 +150,56 @@ def forward_tensorcore(query: torch.Tensor, key: torch.Tensor, value: torch.Tens
     if status != FA2_STATUS_SUCCESS:
         raise Fa2Error("fa2_forward_tensorcore", status, status_string(status))
     return output
+
+
+def _stream_handle(tensor: torch.Tensor, stream: torch.cuda.Stream | None) -> int:
+    return (stream or torch.cuda.current_stream(tensor.device)).cuda_stream
+
+
+def _check(function: str, status: int) -> None:
+    if status != FA2_STATUS_SUCCESS:
+        raise Fa2Error(function, status, status_string(status))
+
+
+def copy(source: torch.Tensor, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """Copy of a contiguous device tensor through fa2_copy."""
+    output = torch.empty_like(source)
+    _check("fa2_copy", lib.fa2_copy(source.data_ptr(), output.data_ptr(),
+                                    source.numel() * source.element_size(),
+                                    _stream_handle(source, stream)))
+    return output
+
+
+def attention_scores_f32(query: torch.Tensor, key: torch.Tensor,
+                         stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """FP32 scores Q K^T / sqrt(D), [B, H, N, N], through fa2_attention_scores_f32."""
+    batch, heads, seq_len, head_dim = query.shape
+    scores = torch.empty((batch, heads, seq_len, seq_len), dtype=torch.float32, device=query.device)
+    _check("fa2_attention_scores_f32",
+           lib.fa2_attention_scores_f32(query.data_ptr(), key.data_ptr(), scores.data_ptr(),
+                                        batch * heads, seq_len, head_dim,
+                                        _stream_handle(query, stream)))
+    return scores
+
+
+def attention_forward_f32(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                          stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """FP32 noncausal attention through fa2_attention_forward_f32."""
+    batch, heads, seq_len, head_dim = query.shape
+    output = torch.empty_like(query)
+    _check("fa2_attention_forward_f32",
+           lib.fa2_attention_forward_f32(query.data_ptr(), key.data_ptr(), value.data_ptr(),
+                                         output.data_ptr(), batch * heads, seq_len, head_dim,
+                                         _stream_handle(query, stream)))
+    return output
+
+
+def matmul_16x64x16(a: torch.Tensor, b: torch.Tensor,
+                    stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """[batch, 16, 64] x [batch, 64, 16] FP16 -> [batch, 16, 16] FP32 through fa2_matmul_16x64x16_f16."""
+    batch = a.shape[0]
+    c = torch.empty((batch, 16, 16), dtype=torch.float32, device=a.device)
+    _check("fa2_matmul_16x64x16_f16",
+           lib.fa2_matmul_16x64x16_f16(a.data_ptr(), b.data_ptr(), c.data_ptr(), batch,
+                                       _stream_handle(a, stream)))
+    return c

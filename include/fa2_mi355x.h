@@ -4,9 +4,11 @@
  * Library: flash_attention_2_lab_amd/libfa2_mi355x.so (hand-written HIP for gfx950).
  *
  * Every entry point takes plain device pointers and sizes; no torch or HIP types
- * appear in the signatures. Tensors are FP16 (IEEE binary16), row-major
- * [batch, heads, seq_len, head_dim], contiguous, 16-byte aligned. The output
- * buffer is written, never read; inputs are read-only. Calls are asynchronous:
+ * appear in the signatures. The attention tensors are row-major
+ * [batch, heads, seq_len, head_dim] and contiguous: FP16 (IEEE binary16) and
+ * 16-byte aligned for the tensor-core entries, FP32 and 4-byte aligned for the
+ * FP32 entries. Output buffers are written, never read; inputs are read-only and
+ * must not overlap the output. Calls are asynchronous:
  * the kernel is enqueued on `stream` (a hipStream_t passed as void*; NULL means
  * the legacy default stream) and no host synchronisation happens.
  *
@@ -23,15 +25,15 @@
 extern "C" {
 #endif
 
-#define FA2_MI355X_ABI_VERSION 2
+#define FA2_MI355X_ABI_VERSION 3
 
 enum fa2_status {
     FA2_STATUS_SUCCESS = 0,
     FA2_STATUS_NULL_POINTER = 1,        /* non-empty problem with a NULL tensor pointer      */
     FA2_STATUS_NEGATIVE_DIMENSION = 2,  /* batch, heads, seq_len or head_dim below zero      */
-    FA2_STATUS_BAD_HEAD_DIM = 3,        /* head_dim != 64                                    */
+    FA2_STATUS_BAD_HEAD_DIM = 3,        /* head_dim not supported by the entry               */
     FA2_STATUS_BAD_SEQUENCE_LENGTH = 4, /* seq_len not a multiple of the entry's key tile    */
-    FA2_STATUS_MISALIGNED = 5,          /* a tensor pointer is not 16-byte aligned           */
+    FA2_STATUS_MISALIGNED = 5,          /* a pointer below the entry's alignment             */
     FA2_STATUS_TOO_LARGE = 6,           /* seq_len > 2^24 or launch grid beyond 2^32 groups */
     FA2_STATUS_BAD_KEY_TILE = 7,        /* fa2_forward_tensorcore: key_tile not 16 or 32     */
     FA2_STATUS_HIP_ERROR_BASE = 1000    /* + hipError_t from the launch                      */
@@ -72,6 +74,45 @@ int fa2_forward_production_128x128(const void* query, const void* key, const voi
 int fa2_forward_tensorcore(const void* query, const void* key, const void* value,
                            void* output, int64_t batch, int64_t heads, int64_t seq_len,
                            int64_t head_dim, int64_t key_tile, void* stream);
+
+/*
+ * Device-to-device copy of `bytes` bytes (src and dst must not overlap).
+ * Replaces copy_cuda (reference csrc/copy_kernel.cu:23-53; binding
+ * csrc/bindings.cpp:71-75), which copies a contiguous floating-point tensor.
+ */
+int fa2_copy(const void* src, void* dst, int64_t bytes, void* stream);
+
+/*
+ * FP32 attention scores S = Q K^T / sqrt(head_dim) for each of batch_heads
+ * [seq_len, head_dim] slabs of Q and K; writes S as [batch_heads, seq_len, seq_len].
+ * Replaces naive_attention_scores (reference csrc/naive_attention.cu:174-201,
+ * 330-418; binding csrc/bindings.cpp:83-87).
+ */
+int fa2_attention_scores_f32(const float* query, const float* key, float* scores,
+                             int64_t batch_heads, int64_t seq_len, int64_t head_dim,
+                             void* stream);
+
+/*
+ * FP32 attention forward, noncausal, O = softmax(Q K^T / sqrt(head_dim)) V, for
+ * head_dim 64 or 128 and any seq_len. Replaces the reference's four FP32 SIMT
+ * forwards, which compute the same attention with different thread mappings:
+ *   naive_attention_forward     (reference csrc/naive_attention.cu:112-172, 249-328)
+ *   block_attention_forward     (csrc/naive_attention.cu:48-110, 420-502)
+ *   tiled_attention_forward     (csrc/tiled_attention.cu:273-333), head_dim 64
+ *   tilewise_attention_forward  (csrc/tilewise_attention.cu:337-388), head_dim 64
+ *   (bindings csrc/bindings.cpp:77-81, 89-105).
+ */
+int fa2_attention_forward_f32(const float* query, const float* key, const float* value,
+                              float* output, int64_t batch_heads, int64_t seq_len,
+                              int64_t head_dim, void* stream);
+
+/*
+ * C[i] = A[i] B[i] for `batch` pairs of a 16x64 and a 64x16 FP16 matrix (row-major,
+ * contiguous), FP32 result [batch, 16, 16]; two v_mfma_f32_16x16x32_f16 per pair.
+ * Replaces wmma_matmul_16x64x16 (reference csrc/wmma_matmul.cu:51-193, 250-315;
+ * binding csrc/bindings.cpp:107-111).
+ */
+int fa2_matmul_16x64x16_f16(const void* a, const void* b, float* c, int64_t batch, void* stream);
 
 /* Human-readable name of a status code returned by this library (static storage). */
 const char* fa2_status_string(int status);

@@ -1,4 +1,4 @@
-"""CPU oracle for the FP16 D=64 attention forward - TEST INFRASTRUCTURE ONLY.
+"""CPU oracle for the attention forward and the module's other operators - TEST INFRASTRUCTURE ONLY.
 
 This package restates the reference's semantics on the CPU so the HIP kernel can be
 checked against them. It is never part of the product path: only ``tests/``,
@@ -20,6 +20,13 @@ Contents (each function cites the reference file:line it restates):
                                    arithmetic: 128-key tiles, FP32 online softmax, P
                                    rounded to FP16 for P.V, FP32 denominator
                                    (csrc/tensorcore_attention.cu:2229-2561, 448-671).
+* ``attention_scores_fp32``      - FP32 Q K^T * s, [B, H, N, N] (naive_attention_scores,
+                                   csrc/naive_attention.cu:174-201, 330-418).
+* ``matmul_16x64x16_fp32``       - FP32 product of [b, 16, 64] and [b, 64, 16] FP16
+                                   matrices (wmma_matmul_16x64x16,
+                                   csrc/wmma_matmul.cu:51-193).
+The FP32 SIMT forwards (naive, block, tiled, tilewise) are checked against
+``attention_reference_fp32``, which is what the reference's tests use for them.
 
 How each is pinned (tests/test_oracle.py):
   attention_reference       - torch's scaled_dot_product_attention on CPU (a library
@@ -32,10 +39,18 @@ How each is pinned (tests/test_oracle.py):
   flash_forward_tiled       - within the kernel tolerance of attention_reference, and
                               exactly equal to it in FP32 when the FP16 rounding of P is
                               switched off and one tile covers the sequence.
+  attention_scores_fp32     - a float64 loop over (i, j, d) on small inputs, and the
+                              known answer of constant per-(batch, head) inputs
+                              (reference tests/test_naive_scores.py:71-107).
+  matmul_16x64x16_fp32      - a float64 loop on random inputs, and the identity-block
+                              known answer A [I; 0] = A[:, :, :16]
+                              (reference tests/test_wmma_matmul.py:13-75).
 """
 
 from oracle.reference import (
     attention_float64_rowwise,
+    attention_scores_fp32,
+    matmul_16x64x16_fp32,
     attention_reference,
     attention_reference_fp32,
     attention_rows_fp32,
@@ -45,6 +60,8 @@ from oracle.reference import (
 
 __all__ = [
     "attention_float64_rowwise",
+    "attention_scores_fp32",
+    "matmul_16x64x16_fp32",
     "attention_reference",
     "attention_reference_fp32",
     "attention_rows_fp32",

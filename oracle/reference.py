@@ -166,3 +166,25 @@ def flash_forward_tiled(query: Tensor, key: Tensor, value: Tensor, *, causal: bo
         acc = alpha * acc + torch.matmul(p_mma, v[:, :, k0:k1])
         m = m_new
     return (acc / l).half()
+
+
+def attention_scores_fp32(query: Tensor, key: Tensor, *, scale: float | None = None) -> Tensor:
+    """FP32 scaled scores Q K^T * s, [B, H, N, N] (reference naive_attention_scores,
+    csrc/naive_attention.cu:174-201 and 330-418; its test formula,
+    tests/test_naive_scores.py:48-54): the product of the FP32-converted inputs,
+    then the scale 1/sqrt(D) unless given."""
+    if query.ndim != 4 or key.ndim != 4:
+        raise ValueError("query and key must have shape [batch, heads, sequence, head_dimension]")
+    s = _default_scale(query.shape[-1], scale)
+    return torch.matmul(query.float().cpu(), key.float().cpu().transpose(-2, -1)) * s
+
+
+def matmul_16x64x16_fp32(matrix_a: Tensor, matrix_b: Tensor) -> Tensor:
+    """FP32 product of [batch, 16, 64] and [batch, 64, 16] FP16 matrices (reference
+    wmma_matmul_16x64x16, csrc/wmma_matmul.cu:51-193: four 16x16x16 FP16 products
+    accumulated in FP32; its test formula, tests/test_wmma_matmul.py:94-120)."""
+    if matrix_a.ndim != 3 or tuple(matrix_a.shape[1:]) != (16, 64):
+        raise ValueError("A must have shape [batch, 16, 64]")
+    if matrix_b.ndim != 3 or tuple(matrix_b.shape[1:]) != (64, 16):
+        raise ValueError("B must have shape [batch, 64, 16]")
+    return torch.matmul(matrix_a.float().cpu(), matrix_b.float().cpu())

@@ -58,6 +58,23 @@ def test_support_predicates_follow_the_reference(n, causal, expected):
     assert not any(s.supported(fp32) for s in bm.KERNELS if s.name.startswith("tensorcore"))
 
 
+@pytest.mark.parametrize("dtype, n, d, causal, expected", [
+    (torch.float32, 100, 64, False, {"naive_online", "block_online", "tiled_simt", "tilewise_simt"}),
+    (torch.float32, 100, 128, False, {"naive_online", "block_online"}),
+    (torch.float32, 100, 64, True, set()),
+    (torch.float32, 96, 32, False, set()),
+    (torch.float16, 128, 64, False, set()),
+])
+def test_simt_support_predicates_follow_the_reference(dtype, n, d, causal, expected):
+    # Reference benchmarks/kernels.py:137-183: FP32, square, D in {64, 128} (naive,
+    # block) or 64 (tiled, tilewise), noncausal.
+    w = bm.AttentionWorkload(1, 8, n, n, d, dtype=dtype, causal=causal)
+    simt = {"naive_online", "block_online", "tiled_simt", "tilewise_simt"}
+    assert {s.name for s in bm.KERNELS if s.name in simt and s.supported(w)} == expected
+    rectangular = bm.AttentionWorkload(1, 8, n, n + 1, 64, dtype=torch.float32)
+    assert not any(bm.find_kernel(name).supported(rectangular) for name in simt)
+
+
 def test_device_sdpa_is_not_offered_in_bfloat16():
     w = bm.AttentionWorkload(1, 8, 128, 128, 64, dtype=torch.bfloat16)
     assert not bm.find_kernel("pytorch_sdpa").supported(w)

@@ -19,7 +19,7 @@ def test_cli_times_the_tensorcore_entries(capsys):
     out = capsys.readouterr().out
     assert status == 0
     assert "Workload: B=1, H=2, Nq=256, Nk=256, D=64, dtype=float16, causal=False" in out
-    assert "naive_online" in out and "not built" in out
+    assert "naive_online" in out and "unsupported" in out  # an FP32 kernel on FP16 inputs
     rows = [json.loads(line) for line in out.splitlines() if line.startswith("{")]
     assert {r["kernel"] for r in rows} == {"tensorcore_production_128x128", "tensorcore_attention",
                                           "tensorcore_attention_bc32"}
@@ -33,3 +33,15 @@ def test_cli_reports_unsupported_and_unknown_kernels(capsys):
                  "--warmup", "0", "--kernels", "tensorcore_production_128x128"]) == 0
     assert "tensorcore_production_128x128" in capsys.readouterr().out
     assert main(["--kernels", "no_such_kernel"]) == 2
+
+
+def test_cli_times_the_fp32_simt_entries(capsys):
+    status = main(["--dtype", "float32", "--heads", "2", "--query-length", "200", "--head-dim", "64",
+                   "--samples", "3", "--iterations", "2", "--warmup", "1", "--json",
+                   "--kernels", "naive_online", "block_online", "tiled_simt", "tilewise_simt",
+                   "tensorcore_attention"])
+    out = capsys.readouterr().out
+    assert status == 0
+    rows = [json.loads(line) for line in out.splitlines() if line.startswith("{")]
+    assert {r["kernel"] for r in rows} == {"naive_online", "block_online", "tiled_simt", "tilewise_simt"}
+    assert "tensorcore_attention" in out and "unsupported" in out

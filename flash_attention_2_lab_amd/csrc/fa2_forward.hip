@@ -876,39 +876,28 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
     const int lq = lane & 31;
     const int half = lane >> 5;
 
-    // Workgroup -> (batch*head, query tile), XCD-contiguous; causal tiles run
-    // heaviest first.
+    // Workgroup -> (batch*head, work item), XCD-contiguous. Noncausal: an item is
+    // one query tile. Causal: an item is the pair of query tiles T-1-p and p of a
+    // head with T tiles, heaviest first, so every workgroup streams the same
+    // 4(T+1) key tiles and the workgroup slots of the chip drain together (one
+    // tile per workgroup left the busiest CUs 25% above the mean).
     const uint32_t groups = gridDim.x;
     const uint32_t xcd = blockIdx.x & 7u;
     const uint32_t slot = blockIdx.x >> 3;
     const uint32_t per_xcd = groups >> 3;
     const uint32_t extra = groups & 7u;
     const uint32_t logical = xcd * per_xcd + min(xcd, extra) + slot;
-    const uint32_t bh = logical / (uint32_t)num_query_tiles;
-    uint32_t qtile = logical - bh * (uint32_t)num_query_tiles;
-    if (kCausal) qtile = (uint32_t)num_query_tiles - 1u - qtile;
+    const uint32_t items = kCausal ? ((uint32_t)num_query_tiles + 1u) / 2u : (uint32_t)num_query_tiles;
+    const uint32_t bh = logical / items;
+    const uint32_t item = logical - bh * items;
+    // With T odd the middle tile is its own pair and runs alone.
+    const int passes = (kCausal && 2u * item + 1u != (uint32_t)num_query_tiles) ? 2 : 1;
 
     const size_t head_offset = (size_t)bh * (size_t)seq_len * kHeadDim;
     const _Float16* __restrict__ q_head = query + head_offset;
     const u32x4 k_head = head_descriptor(key + head_offset, seq_len);
     const u32x4 v_head = head_descriptor(value + head_offset, seq_len);
     _Float16* __restrict__ o_head = output + head_offset;
-
-    const int q_block = (int)qtile * kBlockM;
-    const int q_wave = q_block + wave * kWaveQueries;
-    const int query_a = q_wave + lq;
-    const int query_b = query_a + kQueriesPerWave;
-    const int num_tiles = kCausal ? (q_block + kBlockM - 1) / kKeysPerTile + 1 : seq_len / kKeysPerTile;
-    // Causal: the wave's last tile is its diagonal tile (q_wave is a multiple of 64).
-    const int wave_last_tile = kCausal ? q_wave / kKeysPerTile : num_tiles - 1;
-
-    // Q^T fragments of both blocks (B operands of K Q^T).
-    f16x8 qa[4], qb[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-        qa[ks] = *reinterpret_cast<const f16x8*>(q_head + (size_t)query_a * kHeadDim + ks * 16 + half * 8);
-        qb[ks] = *reinterpret_cast<const f16x8*>(q_head + (size_t)query_b * kHeadDim + ks * 16 + half * 8);
-    }
 
     const uint32_t smem_addr = lds_address(smem);
     const int dma_off[2] = {dma_lane_offset(lane, 0), dma_lane_offset(lane, 1)};
@@ -925,9 +914,6 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
                       t * kTileBytes + r0 * kRowBytes);
         }
     };
-    dma_tile(0);
-    if (num_tiles > 1) dma_tile(1);
-    if (num_tiles > 2) dma_tile(2);
 
     const int k_row = key_of_mfma_row(lq);
     const int k_swz = tile_swizzle(k_row);
@@ -946,16 +932,6 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
             v_off[r][dblk] = row * kRowBytes + ((chunk ^ tile_swizzle(row)) << 4) + 8 * (i16 & 1);
         }
 
-    f32x16 oa[2], ob[2];
-#pragma unroll
-    for (int d = 0; d < 2; ++d)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            oa[d][i] = 0.0f;
-            ob[d][i] = 0.0f;
-        }
-    float m_a = -INFINITY, m_b = -INFINITY;  // running max of raw scores per block
-    float l_a = 0.0f, l_b = 0.0f;            // this lane's share of each denominator
     const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
 
     // Exact tile max of one block and lazy rescale of its l and O (bound
@@ -1004,103 +980,7 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
         return sum;
     };
 
-    // Prologue: tiles 0..2 and Q landed. The empty asm consumes Q where the compiler
-    // adds its own wait for the Q loads: already satisfied here, whereas at the first
-    // MFMA its count would also cover the tile-3 fetch issued in between.
-    wait_dma_and_barrier<0>();
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) asm volatile("" ::"v"(qa[ks]), "v"(qb[ks]));
-
-    for (int t = 0; t < num_tiles; ++t) {
-        if (t + 3 < num_tiles) dma_tile(t + 3);  // into the stage tile t-1 used
-        if (t <= wave_last_tile) {
-            const uint8_t* k_lds = smem + (t & (kStages - 1)) * kStageBytes;
-            const uint8_t* v_lds = k_lds + kTileBytes;
-
-            // S^T = K Q^T of both blocks; each K fragment feeds two MFMAs. The MFMA
-            // phases run at raised wave priority: when both waves of a SIMD can
-            // issue, the one with MFMAs goes first and the other's softmax fills the
-            // MFMA shadow.
-            __builtin_amdgcn_s_setprio(1);
-            f16x8 kf[2][4];
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-                for (int b = 0; b < 2; ++b)
-                    kf[b][ks] = *reinterpret_cast<const f16x8*>(k_lds + b * 32 * kRowBytes + k_off[ks]);
-            f32x16 sa[2], sb[2];
-            const f32x16 zero = {};
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-                for (int b = 0; b < 2; ++b) {
-                    sa[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[b][ks], qa[ks], ks == 0 ? zero : sa[b], 0, 0, 0);
-                    sb[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[b][ks], qb[ks], ks == 0 ? zero : sb[b], 0, 0, 0);
-                }
-            __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_s_setprio(0);
-            // V^T fragments of the tile (P.V MFMA k: key block k/4, 16-key half
-            // (k/2)%2, d-block k%2), read while the softmax runs.
-            f16x8 vf[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int row_base = (32 * (k >> 2) + 16 * ((k >> 1) & 1)) * kRowBytes;
-                const f16x4 v_lo = lds_read_transposed(v_lds + row_base + v_off[0][k & 1]);
-                const f16x4 v_hi = lds_read_transposed(v_lds + row_base + v_off[1][k & 1]);
-                vf[k] = __builtin_shufflevector(v_lo, v_hi, 0, 1, 2, 3, 4, 5, 6, 7);
-            }
-
-            // Causal mask on the wave's diagonal tile (keys 64t.. = q_wave..): register
-            // i of block b holds key 64t + 32b + 16(i/8) + 8*half + i%8.
-            if (kCausal && t == wave_last_tile) {
-#pragma unroll
-                for (int b = 0; b < 2; ++b)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const int key_index = t * kKeysPerTile + 32 * b + 16 * (i >> 3) + 8 * half + (i & 7);
-                        if (key_index > query_a) sa[b][i] = -INFINITY;
-                        if (key_index > query_b) sb[b][i] = -INFINITY;
-                    }
-            }
-
-            // Online softmax per block: exact max on the first tile, then the running
-            // max with the lane-sum check (every probability is <= 2^8 when its lane's
-            // sum is), recomputing only a block whose check fails.
-            f16x8 pa[2][2], pb[2][2];
-            if (t == 0) {
-                exact_max_update(sa, m_a, l_a, oa);
-                exact_max_update(sb, m_b, l_b, ob);
-            }
-            float sum_a = tile_probs(sa, m_a, pa);
-            float sum_b = tile_probs(sb, m_b, pb);
-            if (t != 0) {
-                if (__builtin_amdgcn_ballot_w64(sum_a > 256.0f) != 0 && exact_max_update(sa, m_a, l_a, oa))
-                    sum_a = tile_probs(sa, m_a, pa);
-                if (__builtin_amdgcn_ballot_w64(sum_b > 256.0f) != 0 && exact_max_update(sb, m_b, l_b, ob))
-                    sum_b = tile_probs(sb, m_b, pb);
-            }
-            l_a += sum_a;
-            l_b += sum_b;
-
-            // O^T += V^T P^T for both blocks; each V^T fragment feeds two MFMAs.
-            __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                oa[k & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[k], pa[k >> 2][(k >> 1) & 1], oa[k & 1], 0, 0, 0);
-                ob[k & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[k], pb[k >> 2][(k >> 1) & 1], ob[k & 1], 0, 0, 0);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_s_setprio(0);
-        }
-        // Tile t+1 must have landed; only the fetches of the tiles after it may stay
-        // in flight. After the barrier every wave is done with tile t's stage.
-        if (t + 3 < num_tiles) wait_dma_and_barrier<2 * kDmaPerTile>();
-        else if (t + 2 < num_tiles) wait_dma_and_barrier<kDmaPerTile>();
-        else wait_dma_and_barrier<0>();
-    }
-
-    // Epilogue: O = O^T / l. Accumulator i of d-block dblk holds dim
+    // Epilogue of a pass: O = O^T / l. Accumulator i of d-block dblk holds dim
     // 32*dblk + 8*(i/4) + 4*half + i%4 of the lane's query.
     auto store = [&](const f32x16 (&o)[2], float l_run, int q) {
         const float inv_l = 1.0f / sum_across_halves(l_run);
@@ -1114,8 +994,140 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
                 *reinterpret_cast<f16x4*>(o_row + 32 * dblk + 8 * g + 4 * half) = __builtin_shufflevector(a, c, 0, 1, 2, 3);
             }
     };
-    store(oa, l_a, query_a);
-    store(ob, l_b, query_b);
+
+    for (int pass = 0; pass < passes; ++pass) {
+        const uint32_t qtile = !kCausal ? item : pass == 0 ? (uint32_t)num_query_tiles - 1u - item : item;
+        const int q_block = (int)qtile * kBlockM;
+        const int q_wave = q_block + wave * kWaveQueries;
+        const int query_a = q_wave + lq;
+        const int query_b = query_a + kQueriesPerWave;
+        const int num_tiles = kCausal ? (q_block + kBlockM - 1) / kKeysPerTile + 1 : seq_len / kKeysPerTile;
+        // Causal: the wave's last tile is its diagonal tile (q_wave is a multiple of 64).
+        const int wave_last_tile = kCausal ? q_wave / kKeysPerTile : num_tiles - 1;
+
+        // Q^T fragments of both blocks (B operands of K Q^T). Tiles 0..2 go to stages
+        // 0..2: the previous pass ended with every wave past a barrier after its last
+        // tile, and with no fetch in flight.
+        f16x8 qa[4], qb[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            qa[ks] = *reinterpret_cast<const f16x8*>(q_head + (size_t)query_a * kHeadDim + ks * 16 + half * 8);
+            qb[ks] = *reinterpret_cast<const f16x8*>(q_head + (size_t)query_b * kHeadDim + ks * 16 + half * 8);
+        }
+        dma_tile(0);
+        dma_tile(1);  // num_tiles >= 4: seq_len and the causal key range are multiples of 256
+        dma_tile(2);
+
+        f32x16 oa[2], ob[2];
+#pragma unroll
+        for (int d = 0; d < 2; ++d)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                oa[d][i] = 0.0f;
+                ob[d][i] = 0.0f;
+            }
+        float m_a = -INFINITY, m_b = -INFINITY;  // running max of raw scores per block
+        float l_a = 0.0f, l_b = 0.0f;            // this lane's share of each denominator
+
+        // Prologue: tiles 0..2 and Q landed. The empty asm consumes Q where the compiler
+        // adds its own wait for the Q loads: already satisfied here, whereas at the first
+        // MFMA its count would also cover the tile-3 fetch issued in between.
+        wait_dma_and_barrier<0>();
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) asm volatile("" ::"v"(qa[ks]), "v"(qb[ks]));
+
+        for (int t = 0; t < num_tiles; ++t) {
+            if (t + 3 < num_tiles) dma_tile(t + 3);  // into the stage tile t-1 used
+            if (t <= wave_last_tile) {
+                const uint8_t* k_lds = smem + (t & (kStages - 1)) * kStageBytes;
+                const uint8_t* v_lds = k_lds + kTileBytes;
+
+                // S^T = K Q^T of both blocks; each K fragment feeds two MFMAs. The MFMA
+                // phases run at raised wave priority: when both waves of a SIMD can
+                // issue, the one with MFMAs goes first and the other's softmax fills the
+                // MFMA shadow.
+                __builtin_amdgcn_s_setprio(1);
+                f16x8 kf[2][4];
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                    for (int b = 0; b < 2; ++b)
+                        kf[b][ks] = *reinterpret_cast<const f16x8*>(k_lds + b * 32 * kRowBytes + k_off[ks]);
+                f32x16 sa[2], sb[2];
+                const f32x16 zero = {};
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                    for (int b = 0; b < 2; ++b) {
+                        sa[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[b][ks], qa[ks], ks == 0 ? zero : sa[b], 0, 0, 0);
+                        sb[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[b][ks], qb[ks], ks == 0 ? zero : sb[b], 0, 0, 0);
+                    }
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_s_setprio(0);
+                // V^T fragments of the tile (P.V MFMA k: key block k/4, 16-key half
+                // (k/2)%2, d-block k%2), read while the softmax runs.
+                f16x8 vf[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const int row_base = (32 * (k >> 2) + 16 * ((k >> 1) & 1)) * kRowBytes;
+                    const f16x4 v_lo = lds_read_transposed(v_lds + row_base + v_off[0][k & 1]);
+                    const f16x4 v_hi = lds_read_transposed(v_lds + row_base + v_off[1][k & 1]);
+                    vf[k] = __builtin_shufflevector(v_lo, v_hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                }
+
+                // Causal mask on the wave's diagonal tile (keys 64t.. = q_wave..): register
+                // i of block b holds key 64t + 32b + 16(i/8) + 8*half + i%8.
+                if (kCausal && t == wave_last_tile) {
+#pragma unroll
+                    for (int b = 0; b < 2; ++b)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) {
+                            const int key_index = t * kKeysPerTile + 32 * b + 16 * (i >> 3) + 8 * half + (i & 7);
+                            if (key_index > query_a) sa[b][i] = -INFINITY;
+                            if (key_index > query_b) sb[b][i] = -INFINITY;
+                        }
+                }
+
+                // Online softmax per block: exact max on the first tile, then the running
+                // max with the lane-sum check (every probability is <= 2^8 when its lane's
+                // sum is), recomputing only a block whose check fails.
+                f16x8 pa[2][2], pb[2][2];
+                if (t == 0) {
+                    exact_max_update(sa, m_a, l_a, oa);
+                    exact_max_update(sb, m_b, l_b, ob);
+                }
+                float sum_a = tile_probs(sa, m_a, pa);
+                float sum_b = tile_probs(sb, m_b, pb);
+                if (t != 0) {
+                    if (__builtin_amdgcn_ballot_w64(sum_a > 256.0f) != 0 && exact_max_update(sa, m_a, l_a, oa))
+                        sum_a = tile_probs(sa, m_a, pa);
+                    if (__builtin_amdgcn_ballot_w64(sum_b > 256.0f) != 0 && exact_max_update(sb, m_b, l_b, ob))
+                        sum_b = tile_probs(sb, m_b, pb);
+                }
+                l_a += sum_a;
+                l_b += sum_b;
+
+                // O^T += V^T P^T for both blocks; each V^T fragment feeds two MFMAs.
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    oa[k & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[k], pa[k >> 2][(k >> 1) & 1], oa[k & 1], 0, 0, 0);
+                    ob[k & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[k], pb[k >> 2][(k >> 1) & 1], ob[k & 1], 0, 0, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_s_setprio(0);
+            }
+            // Tile t+1 must have landed; only the fetches of the tiles after it may stay
+            // in flight. After the barrier every wave is done with tile t's stage.
+            if (t + 3 < num_tiles) wait_dma_and_barrier<2 * kDmaPerTile>();
+            else if (t + 2 < num_tiles) wait_dma_and_barrier<kDmaPerTile>();
+            else wait_dma_and_barrier<0>();
+        }
+
+        store(oa, l_a, query_a);
+        store(ob, l_b, query_b);
+    }  // pass
 }
 
 // kPartial instantiations (seq_len not a multiple of the 64-key tile) carry the
@@ -1159,23 +1171,24 @@ template <bool kCausal>
 hipError_t launch_wide(const void* q, const void* k, const void* v, void* o, int64_t batch_heads,
                        int64_t seq_len, float scale_log2, hipStream_t stream) {
     const int64_t query_tiles = seq_len / 256;
-    hipLaunchKernelGGL((fa2_forward_d64_wide_kernel<kCausal>), dim3((unsigned)(batch_heads * query_tiles)),
+    const int64_t items = kCausal ? (query_tiles + 1) / 2 : query_tiles;  // causal: tile pairs
+    hipLaunchKernelGGL((fa2_forward_d64_wide_kernel<kCausal>), dim3((unsigned)(batch_heads * items)),
                        dim3(256), 0, stream, static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
                        static_cast<const _Float16*>(v), static_cast<_Float16*>(o), (int)seq_len,
                        (int)query_tiles, scale_log2);
     return hipGetLastError();
 }
 
-// 256-query workgroups (64 queries per wave) once they fill every workgroup slot
-// of the chip (two per CU) for noncausal problems - below that the 128-query
-// kernel is faster - and from 2048 groups for causal ones, where the waves of a
-// 256-query group idle through up to three diagonal tiles: measured on MI355X,
-// B2 H32 N16384 causal runs 7% faster wide, B16 H16 N4096 causal the same, and
-// B1 H64 N4096 causal 13% slower.
+// 256-query workgroups (64 queries per wave) once the grid fills every workgroup
+// slot of the chip (two per CU); below that the 128-query kernel is faster. A
+// causal workgroup takes a pair of query tiles, so a causal problem needs twice
+// the tiles: measured on MI355X, at 512 workgroups and above the wide kernel runs
+// causal problems 5-12% faster (B16 H16 N1024, B2 H16 N8192, B1 H64 N4096, B16 H16
+// N4096) and at 256 it runs them 11-40% slower (B1 H32 N4096, B1 H8 N16384).
 bool use_wide_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
     if (seq_len % 256 != 0) return false;
-    const int64_t groups = batch_heads * (seq_len / 256);
-    return groups >= (causal ? 2048 : 512);
+    const int64_t tiles = seq_len / 256;
+    return batch_heads * (causal ? (tiles + 1) / 2 : tiles) >= 512;
 }
 
 // 128-query workgroups (4 waves) when they fill the chip (two per CU); otherwise

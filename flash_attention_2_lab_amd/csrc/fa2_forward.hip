@@ -877,21 +877,23 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
     const int half = lane >> 5;
 
     // Workgroup -> (batch*head, work item), XCD-contiguous. Noncausal: an item is
-    // one query tile. Causal: an item is the pair of query tiles T-1-p and p of a
-    // head with T tiles, heaviest first, so every workgroup streams the same
-    // 4(T+1) key tiles and the workgroup slots of the chip drain together (one
-    // tile per workgroup left the busiest CUs 25% above the mean).
+    // one query tile. Causal with an even number T of query tiles per head: an item
+    // is the pair of tiles T-1-p and p, heaviest first, so every workgroup streams
+    // the same 4(T+1) key tiles and the workgroup slots of the chip drain together
+    // (one tile per workgroup left the busiest CUs 25% above the mean). Causal with
+    // T odd: one tile per workgroup, heaviest first (pairing would leave the middle
+    // tile's workgroup with half the work).
     const uint32_t groups = gridDim.x;
     const uint32_t xcd = blockIdx.x & 7u;
     const uint32_t slot = blockIdx.x >> 3;
     const uint32_t per_xcd = groups >> 3;
     const uint32_t extra = groups & 7u;
     const uint32_t logical = xcd * per_xcd + min(xcd, extra) + slot;
-    const uint32_t items = kCausal ? ((uint32_t)num_query_tiles + 1u) / 2u : (uint32_t)num_query_tiles;
+    const bool paired = kCausal && (num_query_tiles & 1) == 0;
+    const uint32_t items = paired ? (uint32_t)num_query_tiles / 2u : (uint32_t)num_query_tiles;
     const uint32_t bh = logical / items;
     const uint32_t item = logical - bh * items;
-    // With T odd the middle tile is its own pair and runs alone.
-    const int passes = (kCausal && 2u * item + 1u != (uint32_t)num_query_tiles) ? 2 : 1;
+    const int passes = paired ? 2 : 1;
 
     const size_t head_offset = (size_t)bh * (size_t)seq_len * kHeadDim;
     const _Float16* __restrict__ q_head = query + head_offset;
@@ -1171,7 +1173,7 @@ template <bool kCausal>
 hipError_t launch_wide(const void* q, const void* k, const void* v, void* o, int64_t batch_heads,
                        int64_t seq_len, float scale_log2, hipStream_t stream) {
     const int64_t query_tiles = seq_len / 256;
-    const int64_t items = kCausal ? (query_tiles + 1) / 2 : query_tiles;  // causal: tile pairs
+    const int64_t items = kCausal && query_tiles % 2 == 0 ? query_tiles / 2 : query_tiles;  // causal: tile pairs
     hipLaunchKernelGGL((fa2_forward_d64_wide_kernel<kCausal>), dim3((unsigned)(batch_heads * items)),
                        dim3(256), 0, stream, static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
                        static_cast<const _Float16*>(v), static_cast<_Float16*>(o), (int)seq_len,
@@ -1181,14 +1183,18 @@ hipError_t launch_wide(const void* q, const void* k, const void* v, void* o, int
 
 // 256-query workgroups (64 queries per wave) once the grid fills every workgroup
 // slot of the chip (two per CU); below that the 128-query kernel is faster. A
-// causal workgroup takes a pair of query tiles, so a causal problem needs twice
-// the tiles: measured on MI355X, at 512 workgroups and above the wide kernel runs
-// causal problems 5-12% faster (B16 H16 N1024, B2 H16 N8192, B1 H64 N4096, B16 H16
-// N4096) and at 256 it runs them 11-40% slower (B1 H32 N4096, B1 H8 N16384).
+// causal workgroup takes a pair of query tiles when a head has an even number of
+// them, so such a problem needs twice the tiles: measured on MI355X, at 512
+// workgroups and above the wide kernel runs causal problems 5-12% faster (B16 H16
+// N1024, B2 H16 N8192, B1 H64 N4096, B16 H16 N4096) and at 256 it runs them 11-40%
+// slower (B1 H32 N4096, B1 H8 N16384). Causal problems with an odd number of tiles
+// per head run one tile per workgroup, and only from 2048 workgroups, where that
+// schedule was measured no slower than the 128-query kernel.
 bool use_wide_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
     if (seq_len % 256 != 0) return false;
     const int64_t tiles = seq_len / 256;
-    return batch_heads * (causal ? (tiles + 1) / 2 : tiles) >= 512;
+    if (causal && tiles % 2 != 0) return batch_heads * tiles >= 2048;
+    return batch_heads * (causal ? tiles / 2 : tiles) >= 512;
 }
 
 // 128-query workgroups (4 waves) when they fill the chip (two per CU); otherwise

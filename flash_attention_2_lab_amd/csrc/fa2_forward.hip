@@ -33,7 +33,9 @@
 //    data movement buys clock.
 //  * Workgroup ids are remapped so all query tiles of one (batch, head) land on the
 //    same XCD (dispatch is round-robin over the 8 XCDs), keeping that head's K/V
-//    resident in one L2; causal tiles run heaviest first.
+//    resident in one L2; causal tiles run heaviest first, and the wide variant
+//    runs a head's causal tiles T-1-p and p in one workgroup (T even), so every
+//    workgroup streams the same number of key tiles.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>

@@ -18,7 +18,9 @@ Also reported (extra keys, each timed the same way after the main region):
 `north_star` - B16 H16 N4096 noncausal and causal (the >=50%-of-MFMA-peak target)
 and B2 H32 N16384 causal with sigma=2 logits; `cpu_baseline` - the oracle's FP32
 CPU restatement of the reference (oracle.attention_reference) timed on this host's
-cores on a bounded sample of the same workload.
+cores on a bounded sample of the same workload; `graph_us` - the same K calls per
+mode captured once in a HIP graph and replayed (per-call time, median of three
+replays), for callers that capture launch-bound loops.
 
 FLOPs: 4*B*H*N^2*D per forward, halved for causal. Bytes: 8*B*H*N*D (read Q, K, V
 and write O once, FP16).
@@ -85,6 +87,38 @@ def time_kernel_batches(entry, inputs, modes, steps, warmup):
     per_kernel = {("causal" if causal else "noncausal"): events[i].elapsed_time(events[i + 1]) / 1e3 / steps
                   for i, causal in enumerate(modes)}
     return wall, per_kernel
+
+
+def time_in_graph(entry, inputs, modes, steps, replays=3):
+    """Captures `steps` back-to-back calls per mode in one HIP graph each and times
+    replays with HIP events. Returns {mode: median per-call seconds}."""
+    import torch
+
+    q, k, v = inputs
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # capture needs the lazy setup done off the capture stream
+        for causal in modes:
+            entry(q, k, v, causal)
+    torch.cuda.current_stream().wait_stream(side)
+    result = {}
+    for causal in modes:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(steps):
+                entry(q, k, v, causal)
+        graph.replay()
+        times = []
+        for _ in range(replays):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) / 1e3 / steps)
+        result["causal" if causal else "noncausal"] = sorted(times)[len(times) // 2]
+        del graph
+    return result
 
 
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
@@ -247,6 +281,8 @@ def main() -> int:
                          hbm_frac=round(attention_bytes(1, 8, 1024, 64) / per_kernel[dominant]
                                         / 1e9 / MI355X_HBM_GBPS, 5)),
     }
+    graph = time_in_graph(entry, inputs, modes, args.steps)
+    line["graph_us"] = {m: round(t * 1e6, 3) for m, t in graph.items()}
     del inputs
 
     if not args.skip_north_star:

@@ -217,6 +217,34 @@ def test_runs_on_the_current_stream():
     assert torch.equal(via_c_abi, expected)
 
 
+@pytest.mark.parametrize("shape, causal", [((1, 8, 1024), False), ((1, 8, 1024), True),
+                                           ((8, 16, 1024), False), ((8, 64, 1024), True)])
+def test_forward_replays_in_a_hip_graph(shape, causal):
+    # The forward launches one kernel on the current stream and allocates nothing but
+    # its output, so it can be captured in a HIP graph (the bench size is bound by
+    # launch overhead). Each replay gets new inputs copied into the captured buffers,
+    # with eager work and a synchronization in between, and must equal the eager call
+    # bitwise. Shapes: key-split kernel (B1 H8 N1024) and the 256-query kernel.
+    static = [t.cuda() for t in _inputs(*shape, seed=21)]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            ENTRY(*static, causal)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = ENTRY(*static, causal)
+    for seed in (22, 23, 24):
+        fresh = [t.cuda() for t in _inputs(*shape, seed=seed)]
+        for dst, src in zip(static, fresh):
+            dst.copy_(src)
+        graph.replay()
+        eager = ENTRY(*fresh, causal)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), seed
+
+
 @pytest.mark.parametrize("shape", [(0, 2, 128, 64), (1, 0, 128, 64), (2, 3, 0, 64)])
 def test_empty_inputs_return_empty_output(shape):
     x = torch.empty(shape, device="cuda", dtype=torch.float16)

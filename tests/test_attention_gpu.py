@@ -164,14 +164,15 @@ def test_growing_scores_match_oracle(shape, causal):
 
 @pytest.mark.parametrize("ramp", [False, True])
 @pytest.mark.parametrize("causal, shape", [(False, (8, 16, 1024)), (True, (8, 64, 1024)),
-                                             (True, (2, 64, 2048)), (True, (4, 128, 1280))])
+                                             (True, (2, 64, 2048)), (True, (4, 128, 1280)),
+                                             (True, (8, 64, 512))])
 def test_wide_workgroup_shapes_match_oracle(causal, shape, ramp):
     # Large enough for the 256-query kernel (64 queries per wave as two 32-query
     # blocks): every row of three whole heads - all four waves, both blocks of each
     # wave and, causal, every diagonal tile - plus sampled rows of the others. With
     # `ramp` the key norms grow 5x along the sequence, forcing the recompute path.
-    # Causal workgroups run query tiles T-1-p then p of a head with T even (T = 4 and
-    # 8 here, the second at the smallest paired grid), one tile each with T odd (5).
+    # Causal workgroups run query tiles T-1-p then p of a head with T even (T = 2, 4
+    # and 8 here, T = 8 at the smallest paired grid), one tile each with T odd (5).
     batch, heads, seq_len = shape
     q, k, v = _inputs(*shape, seed=13)
     if ramp:

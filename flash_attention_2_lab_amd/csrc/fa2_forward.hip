@@ -53,7 +53,12 @@ constexpr int kKeysPerTile = 64;                          // BN
 constexpr int kRowBytes = kHeadDim * 2;                   // 128 B per key row
 constexpr int kTileBytes = kKeysPerTile * kRowBytes;      // 8 KiB
 constexpr int kQueryTileAlign = 128;                      // reference kProductionBlockM/N
-constexpr float kRescaleLog2 = 8.0f;                      // lazy-rescale threshold, log2 units
+constexpr float kRescaleLog2 = 14.0f;                     // lazy-rescale threshold, log2 units
+// A lane's probabilities are all <= 2^kRescaleLog2 when their sum is. The row sums
+// add probability pairs in FP16 first, which stays finite for this bound:
+// 2 * 2^14 = 2^15 < 65504.
+constexpr float kTileSumBound = 16384.0f;                 // 2^kRescaleLog2
+static_assert(kTileSumBound == 16384.0f && kRescaleLog2 == 14.0f, "kTileSumBound is 2^kRescaleLog2");
 constexpr int64_t kMaxSeqLen = (int64_t)1 << 24;          // seq_len * 128 B fits in int32
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -348,14 +353,12 @@ void fa2_forward_d64_kernel(const _Float16* __restrict__ query,
     // when their sum is, so one compare of the tile's row sum replaces the row max
     // in the common case; only when some lane's sum exceeds the bound is the exact
     // tile max taken (decide_rescale) and the tile's probabilities recomputed.
-    constexpr float kTileSumBound = 256.0f;  // 2^kRescaleLog2
-    static_assert(kRescaleLog2 == 8.0f, "kTileSumBound is 2^kRescaleLog2");
     // Redo tile `s` after a failed check: exact max, rescale of l and O, and both
     // blocks' probabilities against the new max. Returns the tile's lane sum.
     auto refresh_tile = [&](const f32x16 (&s)[2], f16x8 (&p0)[2], f16x8 (&p1)[2], float tile_sum) -> float {
         float alpha;
         const float tile_max = partial_max(s[1], 0, 16, partial_max(s[0], 0, 16, -INFINITY));
-        if (!decide_rescale(tile_max, alpha)) return tile_sum;  // every probability is <= 2^8
+        if (!decide_rescale(tile_max, alpha)) return tile_sum;  // every probability is <= 2^kRescaleLog2
         rescale_o(alpha);
         const float m_scaled = m_run * scale_log2;
         float sum = 0.0f;
@@ -774,13 +777,13 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_splitk_kernel(const _
 
         // Online softmax with the lazy rescale (bound 2^kRescaleLog2). The first tile
         // of the wave takes the exact max; later tiles use the running max and check
-        // the lane sums (every probability is <= 2^8 when its lane's sum is), taking
+        // the lane sums (every probability is <= 2^kRescaleLog2 when its lane's sum is), taking
         // the exact max and recomputing only when a sum exceeds the bound.
         f16x8 pf[kBlocks][2];
         const bool first = t == t_begin;
         if (first) exact_max_update(sc);
         float tile_sum = tile_probs(sc, pf);
-        if (!first && __builtin_amdgcn_ballot_w64(tile_sum > 256.0f) != 0) {
+        if (!first && __builtin_amdgcn_ballot_w64(tile_sum > kTileSumBound) != 0) {
             if (exact_max_update(sc)) tile_sum = tile_probs(sc, pf);
         }
         l_run += tile_sum;
@@ -1093,7 +1096,7 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
                 }
 
                 // Online softmax per block: exact max on the first tile, then the running
-                // max with the lane-sum check (every probability is <= 2^8 when its lane's
+                // max with the lane-sum check (every probability is <= 2^kRescaleLog2 when its lane's
                 // sum is), recomputing only a block whose check fails.
                 f16x8 pa[2][2], pb[2][2];
                 if (t == 0) {
@@ -1103,9 +1106,9 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
                 float sum_a = tile_probs(sa, m_a, pa);
                 float sum_b = tile_probs(sb, m_b, pb);
                 if (t != 0) {
-                    if (__builtin_amdgcn_ballot_w64(sum_a > 256.0f) != 0 && exact_max_update(sa, m_a, l_a, oa))
+                    if (__builtin_amdgcn_ballot_w64(sum_a > kTileSumBound) != 0 && exact_max_update(sa, m_a, l_a, oa))
                         sum_a = tile_probs(sa, m_a, pa);
-                    if (__builtin_amdgcn_ballot_w64(sum_b > 256.0f) != 0 && exact_max_update(sb, m_b, l_b, ob))
+                    if (__builtin_amdgcn_ballot_w64(sum_b > kTileSumBound) != 0 && exact_max_update(sb, m_b, l_b, ob))
                         sum_b = tile_probs(sb, m_b, pb);
                 }
                 l_a += sum_a;

@@ -150,13 +150,38 @@ def test_long_context_b2_h32_n16384_sigma2_causal():
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("shape", [(1, 64, 1024), (1, 8, 1024)])
 def test_growing_scores_match_oracle(shape, causal):
-    # Key norms ramp up 5x along the sequence, so the running max keeps growing and
-    # the kernels' stale-max probabilities overflow the tile-sum bound tile after
-    # tile: exercises the exact-max recompute path (both the 128-query and the
-    # key-split kernels).
+    # Key norms ramp up 12x along the sequence, so the running max keeps growing (by
+    # some 50 log2 units over a row) and the kernels' stale-max probabilities overflow
+    # the 2^14 tile-sum bound several times per row: exercises the exact-max
+    # recompute path (both the 128-query and the key-split kernels).
     q, k, v = _inputs(*shape, seed=9)
-    ramp = torch.linspace(1.0, 5.0, shape[2]).view(1, 1, -1, 1)
+    ramp = torch.linspace(1.0, 12.0, shape[2]).view(1, 1, -1, 1)
     k = (k.float() * ramp).half()
+    out = _run(q, k, v, causal)
+    assert torch.isfinite(out).all()
+    _assert_close_to_oracle(out, attention_reference_fp32(q, k, v, causal=causal))
+
+
+@pytest.mark.parametrize("step", [13.5, 14.5])
+@pytest.mark.parametrize("causal, shape", [(False, (1, 8, 1024)), (True, (1, 8, 1024)),
+                                           (False, (1, 64, 1024)), (True, (1, 64, 1024)),
+                                           (False, (8, 16, 1024)), (True, (8, 64, 1024))])
+def test_scores_stepping_across_the_rescale_bound(causal, shape, step):
+    # The kernels keep a stale running max until some probability would exceed 2^14
+    # (2^14 + 2^14 is the largest pair their FP16 row sums add without overflow).
+    # Keys 0..63 score 0 and every later key scores `step` log2 units higher, so after
+    # the first key tile each probability is 2^13.5 (kept: the tile sums fail the
+    # check but the exact max stays within the bound) or 2^14.5 (rescaled). A bound
+    # above 2^14 would overflow those pair sums to inf. Key-split, 128-query and
+    # 256-query kernels.
+    batch, heads, seq_len = shape
+    gen = torch.Generator().manual_seed(17)
+    q = torch.ones(batch, heads, seq_len, 64).half()
+    scale_log2 = 1.4426950408889634 / 8.0
+    level = step / (64.0 * scale_log2)          # q.k = 64 * level for keys >= 64
+    k = torch.full((batch, heads, seq_len, 64), level).half()
+    k[:, :, :64] = 0.0
+    v = torch.randn(batch, heads, seq_len, 64, generator=gen).half()
     out = _run(q, k, v, causal)
     assert torch.isfinite(out).all()
     _assert_close_to_oracle(out, attention_reference_fp32(q, k, v, causal=causal))

@@ -1,0 +1,65 @@
+"""GPU parity on both sides of every kernel-choice threshold of the forward.
+
+The forward picks its kernel from (batch*heads, seq_len, causal) (fa2_forward.hip,
+`forward`): the 256-query kernel from 512 workgroups (causal: pairs of query tiles
+when a head has an even number of them, else one tile per workgroup from 2048), the
+128-query kernel from 256 (noncausal) or 512 (causal) groups of 128 queries, and
+otherwise the key-split kernel with 64-key tiles up to 256 query blocks of 32 and
+32-key tiles beyond. Each case below sits one step below or at a threshold; every
+row of the first and last head and sampled rows of the others are checked against the
+FP32 oracle (atol 2e-3 + rtol 1e-2).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import flash_attention_2_lab_amd as fa
+from oracle import attention_rows_fp32
+
+pytestmark = pytest.mark.gpu
+
+ENTRY = fa.flash_attention_cuda.tensorcore_attention_forward_production_128x128
+
+CASES = [
+    # (batch, heads, seq_len, causal, kernel it runs)
+    (1, 127, 1024, False, "128-query (508 groups of 256)"),
+    (1, 128, 1024, False, "256-query (512 groups of 256)"),
+    (1, 31, 1024, False, "key-split, 32-key tiles (248 groups of 128)"),
+    (1, 32, 1024, False, "128-query (256 groups of 128)"),
+    (1, 8, 1024, False, "key-split, 64-key tiles (256 query blocks)"),
+    (1, 9, 1024, False, "key-split, 32-key tiles (288 query blocks)"),
+    (1, 255, 1024, True, "128-query (510 tile pairs)"),
+    (1, 256, 1024, True, "256-query, tile pairs (512 pairs)"),
+    (1, 409, 1280, True, "128-query (2045 single tiles, odd count per head)"),
+    (1, 410, 1280, True, "256-query, single tiles (2050, odd count per head)"),
+    (1, 63, 1024, True, "key-split, 32-key tiles (504 groups of 128)"),
+    (1, 64, 1024, True, "128-query (512 groups of 128)"),
+    (1, 8, 1024, True, "key-split, 64-key tiles (256 query blocks)"),
+    (3, 3, 1024, True, "key-split, 32-key tiles (288 query blocks)"),
+]
+
+
+def _inputs(batch, heads, seq_len, seed):
+    gen = torch.Generator().manual_seed(seed)
+    shape = (batch, heads, seq_len, 64)
+    return tuple(torch.randn(shape, generator=gen).half() for _ in range(3))
+
+
+@pytest.mark.parametrize("batch, heads, seq_len, causal, kernel", CASES,
+                         ids=[("causal: " if c[3] else "noncausal: ") + c[4] for c in CASES])
+def test_threshold_shapes_match_oracle(batch, heads, seq_len, causal, kernel):
+    q, k, v = _inputs(batch, heads, seq_len, seed=31)
+    out = ENTRY(q.cuda(), k.cuda(), v.cuda(), causal)
+    torch.cuda.synchronize()
+    out = out.cpu()
+    assert torch.isfinite(out).all()
+    gen = torch.Generator().manual_seed(32)
+    rows = [(0, 0, i) for i in range(seq_len)] + [(batch - 1, heads - 1, i) for i in range(seq_len)]
+    rows += [(int(torch.randint(batch, (1,), generator=gen)), int(torch.randint(heads, (1,), generator=gen)),
+              int(torch.randint(seq_len, (1,), generator=gen))) for _ in range(96)]
+    rows = sorted(set(rows))
+    expected = attention_rows_fp32(q, k, v, rows, causal=causal)
+    actual = torch.stack([out[b, h, i] for b, h, i in rows]).float()
+    torch.testing.assert_close(actual, expected, atol=2e-3, rtol=1e-2)

@@ -10,7 +10,10 @@
  * FP32 entries. Output buffers are written, never read; inputs are read-only and
  * must not overlap the output. Calls are asynchronous:
  * the kernel is enqueued on `stream` (a hipStream_t passed as void*; NULL means
- * the legacy default stream) and no host synchronisation happens.
+ * the legacy default stream) and no host synchronisation happens. The kernel runs
+ * on the calling thread's current HIP device (hipSetDevice); the pointers and the
+ * stream must belong to that device. The entries allocate nothing and issue no
+ * memset, so they may be recorded into a HIP graph.
  *
  * Status codes: 0 on success; a positive FA2_STATUS_* value for an argument the
  * library rejects before touching the GPU; FA2_STATUS_HIP_ERROR_BASE + hipError_t

@@ -136,6 +136,35 @@ def test_throughput_shape_b16_h16_n4096(causal):
         assert torch.equal(out[:, :, 0], v[:, :, 0])
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_full_size_properties_b16_h16_n4096(causal):
+    # Size-independent properties at the throughput shape, on the device, with no oracle:
+    # * linearity in V - the probabilities depend on Q and K only, so the FP32 O of
+    #   v1 + v2 is the sum of those of v1 and v2 up to summation order and the FP16
+    #   rounding of v1 + v2 itself; the three FP16 outputs add their own roundings
+    #   (|O| < 4: at most 2^-10 each), held to 4e-3;
+    # * noncausal: permuting the query rows permutes the output rows, and permuting keys
+    #   and values together leaves the output unchanged (north-star gate: a wave's
+    #   rescale decisions are shared by its 64 queries, and the key order changes the
+    #   summation order, so neither is bitwise).
+    q, k, v = (t.cuda() for t in _inputs(16, 16, 4096, seed=41))
+    gen = torch.Generator().manual_seed(42)
+    v2 = torch.randn(v.shape, generator=gen).half().cuda()
+    out1, out2, out12 = (ENTRY(q, k, vv, causal) for vv in (v, v2, v + v2))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out12).all()
+    lin = (out1.float() + out2.float() - out12.float()).abs().max().item()
+    assert lin <= 4e-3, lin
+    if causal:
+        return
+    perm = torch.randperm(4096, generator=gen).cuda()
+    out_q = ENTRY(q[:, :, perm].contiguous(), k, v, False)
+    out_kv = ENTRY(q, k[:, :, perm].contiguous(), v[:, :, perm].contiguous(), False)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out_q.float(), out1[:, :, perm].float(), atol=ATOL, rtol=RTOL)
+    torch.testing.assert_close(out_kv.float(), out1.float(), atol=ATOL, rtol=RTOL)
+
+
 def test_long_context_b2_h32_n16384_sigma2_causal():
     q, k, v = _inputs(2, 32, 16384, seed=0, sigma=2.0)
     out = _run(q, k, v, True).cpu()

@@ -28,6 +28,14 @@ FA2_STATUS_TOO_LARGE = 6
 FA2_STATUS_BAD_KEY_TILE = 7
 FA2_STATUS_HIP_ERROR_BASE = 1000
 
+# Kernels of the FP16 forward entries (fa2_forward_plan).
+FA2_KERNEL_NONE = 0
+FA2_KERNEL_256_QUERY = 1
+FA2_KERNEL_256_QUERY_PAIRS = 2
+FA2_KERNEL_128_QUERY = 3
+FA2_KERNEL_KEY_SPLIT_64 = 4
+FA2_KERNEL_KEY_SPLIT_32 = 5
+
 
 class Fa2Error(RuntimeError):
     """A non-zero status from the C ABI."""
@@ -75,6 +83,8 @@ def _load() -> ctypes.CDLL:
     lib.fa2_status_string.restype = ctypes.c_char_p
     lib.fa2_abi_version.argtypes = []
     lib.fa2_abi_version.restype = ctypes.c_int
+    lib.fa2_forward_plan.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int]
+    lib.fa2_forward_plan.restype = ctypes.c_int
     return lib
 
 
@@ -94,6 +104,11 @@ def status_string(status: int) -> str:
 
 def abi_version() -> int:
     return lib.fa2_abi_version()
+
+
+def forward_plan(batch: int, heads: int, seq_len: int, causal: bool) -> int:
+    """FA2_KERNEL_* the FP16 forward entries launch for these sizes (no GPU work)."""
+    return lib.fa2_forward_plan(batch, heads, seq_len, int(causal))
 
 
 def forward_production_128x128_raw(query_ptr: int, key_ptr: int, value_ptr: int,

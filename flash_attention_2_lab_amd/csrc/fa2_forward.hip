@@ -1217,6 +1217,16 @@ bool use_128_query_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
 
 constexpr int64_t kSplitWideMaxBlocks = 256;
 
+// The kernel a forward call with these sizes runs (the single place the choice is made).
+fa2_forward_kernel choose_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
+    if (use_wide_kernel(batch_heads, seq_len, causal))
+        return causal && (seq_len / 256) % 2 == 0 ? FA2_KERNEL_256_QUERY_PAIRS : FA2_KERNEL_256_QUERY;
+    if (seq_len % kQueryTileAlign == 0 && use_128_query_kernel(batch_heads, seq_len, causal))
+        return FA2_KERNEL_128_QUERY;
+    const int64_t query_blocks = (seq_len + kQueriesPerWave - 1) / kQueriesPerWave;
+    return batch_heads * query_blocks <= kSplitWideMaxBlocks ? FA2_KERNEL_KEY_SPLIT_64 : FA2_KERNEL_KEY_SPLIT_32;
+}
+
 bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) != 0; }
 
 
@@ -1245,20 +1255,25 @@ int forward(const void* query, const void* key, const void* value, void* output,
     const float scale = 1.0f / sqrtf((float)kHeadDim);           // reference :3040-3046
     const float scale_log2 = scale * 1.4426950408889634074f;     // fold log2(e) for exp2
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const bool full_tiles = seq_len % kQueryTileAlign == 0;
     hipError_t err;
-    if (use_wide_kernel(batch_heads, seq_len, causal)) {
-        err = causal ? launch_wide<true>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
-                     : launch_wide<false>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
-    } else if (full_tiles && use_128_query_kernel(batch_heads, seq_len, causal)) {
-        err = causal ? launch_forward<true, 4>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
-                     : launch_forward<false, 4>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
-    } else if (batch_heads * query_blocks <= kSplitWideMaxBlocks) {
-        err = causal ? launch_splitk<true, 4, 2>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
-                     : launch_splitk<false, 4, 2>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
-    } else {
-        err = causal ? launch_splitk<true, 4, 1>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
-                     : launch_splitk<false, 4, 1>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
+    switch (choose_kernel(batch_heads, seq_len, causal)) {
+        case FA2_KERNEL_256_QUERY:
+        case FA2_KERNEL_256_QUERY_PAIRS:
+            err = causal ? launch_wide<true>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
+                         : launch_wide<false>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
+            break;
+        case FA2_KERNEL_128_QUERY:
+            err = causal ? launch_forward<true, 4>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
+                         : launch_forward<false, 4>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
+            break;
+        case FA2_KERNEL_KEY_SPLIT_64:
+            err = causal ? launch_splitk<true, 4, 2>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
+                         : launch_splitk<false, 4, 2>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
+            break;
+        default:
+            err = causal ? launch_splitk<true, 4, 1>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
+                         : launch_splitk<false, 4, 1>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
+            break;
     }
     return err == hipSuccess ? FA2_STATUS_SUCCESS : FA2_STATUS_HIP_ERROR_BASE + (int)err;
 }
@@ -1297,6 +1312,15 @@ extern "C" const char* fa2_status_string(int status) {
     if (status > FA2_STATUS_HIP_ERROR_BASE)
         return hipGetErrorString(static_cast<hipError_t>(status - FA2_STATUS_HIP_ERROR_BASE));
     return "unknown status";
+}
+
+extern "C" int fa2_forward_plan(int64_t batch, int64_t heads, int64_t seq_len, int causal) {
+    if (batch <= 0 || heads <= 0 || seq_len <= 0) return FA2_KERNEL_NONE;
+    if (seq_len > kMaxSeqLen || batch > (int64_t)UINT32_MAX / heads) return FA2_KERNEL_NONE;
+    const int64_t batch_heads = batch * heads;
+    const int64_t query_blocks = (seq_len + kQueriesPerWave - 1) / kQueriesPerWave;
+    if (batch_heads > (int64_t)UINT32_MAX / query_blocks) return FA2_KERNEL_NONE;
+    return choose_kernel(batch_heads, seq_len, causal != 0);
 }
 
 extern "C" int fa2_abi_version(void) { return FA2_MI355X_ABI_VERSION; }

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define FA2_MI355X_ABI_VERSION 3
+#define FA2_MI355X_ABI_VERSION 4
 
 enum fa2_status {
     FA2_STATUS_SUCCESS = 0,
@@ -122,6 +122,26 @@ const char* fa2_status_string(int status);
 
 /* FA2_MI355X_ABI_VERSION of the loaded library. */
 int fa2_abi_version(void);
+
+/* Kernels of the FP16 forward entries (fa2_forward_plan). */
+enum fa2_forward_kernel {
+    FA2_KERNEL_NONE = 0,             /* empty or rejected sizes: nothing is launched       */
+    FA2_KERNEL_256_QUERY = 1,        /* 256 queries per workgroup, one query tile each     */
+    FA2_KERNEL_256_QUERY_PAIRS = 2,  /* 256 queries per workgroup, causal tiles T-1-p, p   */
+    FA2_KERNEL_128_QUERY = 3,        /* 128 queries per workgroup                          */
+    FA2_KERNEL_KEY_SPLIT_64 = 4,     /* 32 queries per workgroup, keys split over 4 waves, */
+                                     /* 64-key tiles                                       */
+    FA2_KERNEL_KEY_SPLIT_32 = 5      /* the same with 32-key tiles                         */
+};
+
+/*
+ * The kernel fa2_forward_production_128x128 and fa2_forward_tensorcore launch for
+ * these sizes (head_dim 64, any accepted seq_len; causal for the production entry
+ * only), or FA2_KERNEL_NONE when they launch nothing. No GPU work, no HIP call.
+ * No counterpart in the reference (whose production entry has one kernel): it is
+ * for callers and tests that need to know which schedule a shape gets.
+ */
+int fa2_forward_plan(int64_t batch, int64_t heads, int64_t seq_len, int causal);
 
 #ifdef __cplusplus
 }

@@ -36,6 +36,41 @@ def test_status_codes_match_header():
         assert getattr(capi, f"FA2_STATUS_{name}") == value
 
 
+def test_kernel_ids_match_header():
+    text = capi.HEADER_PATH.read_text()
+    for name in ("NONE", "256_QUERY", "256_QUERY_PAIRS", "128_QUERY", "KEY_SPLIT_64", "KEY_SPLIT_32"):
+        value = int(re.search(rf"FA2_KERNEL_{name} = (\d+)", text).group(1))
+        assert getattr(capi, f"FA2_KERNEL_{name}") == value
+
+
+K = capi
+
+
+@pytest.mark.parametrize("batch, heads, seq_len, causal, kernel", [
+    # Noncausal: 256-query from 512 groups of 256 queries, 128-query from 256 groups of
+    # 128, key-split below (64-key tiles up to 256 blocks of 32 queries).
+    (1, 128, 1024, False, K.FA2_KERNEL_256_QUERY), (1, 127, 1024, False, K.FA2_KERNEL_128_QUERY),
+    (16, 16, 4096, False, K.FA2_KERNEL_256_QUERY), (1, 32, 1024, False, K.FA2_KERNEL_128_QUERY),
+    (1, 31, 1024, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 8, 1024, False, K.FA2_KERNEL_KEY_SPLIT_64),
+    (1, 9, 1024, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 8, 128, False, K.FA2_KERNEL_KEY_SPLIT_64),
+    # Causal: pairs of 256-query tiles from 512 workgroups when a head has an even
+    # number of tiles, single tiles from 2048 with an odd number.
+    (16, 16, 4096, True, K.FA2_KERNEL_256_QUERY_PAIRS), (1, 256, 1024, True, K.FA2_KERNEL_256_QUERY_PAIRS),
+    (1, 255, 1024, True, K.FA2_KERNEL_128_QUERY), (2, 32, 16384, True, K.FA2_KERNEL_256_QUERY_PAIRS),
+    (1, 410, 1280, True, K.FA2_KERNEL_256_QUERY), (1, 409, 1280, True, K.FA2_KERNEL_128_QUERY),
+    (1, 64, 1024, True, K.FA2_KERNEL_128_QUERY), (1, 63, 1024, True, K.FA2_KERNEL_KEY_SPLIT_32),
+    (1, 8, 1024, True, K.FA2_KERNEL_KEY_SPLIT_64),
+    # Sequence lengths the production entry rejects but the Bc16/Bc32 entries take
+    # (partial last block) run the key-split kernel.
+    (4, 64, 1040, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 2, 80, False, K.FA2_KERNEL_KEY_SPLIT_64),
+    # Nothing to launch.
+    (0, 8, 1024, False, K.FA2_KERNEL_NONE), (1, 0, 1024, True, K.FA2_KERNEL_NONE),
+    (1, 8, 0, False, K.FA2_KERNEL_NONE), (1, 1, (1 << 24) + 128, False, K.FA2_KERNEL_NONE),
+])
+def test_forward_plan_follows_the_measured_thresholds(batch, heads, seq_len, causal, kernel):
+    assert capi.forward_plan(batch, heads, seq_len, causal) == kernel
+
+
 @pytest.mark.parametrize("status, text", [
     (capi.FA2_STATUS_SUCCESS, "success"),
     (capi.FA2_STATUS_BAD_HEAD_DIM, "head dimension must equal 64"),

@@ -5,9 +5,10 @@ The forward picks its kernel from (batch*heads, seq_len, causal) (fa2_forward.hi
 when a head has an even number of them, else one tile per workgroup from 2048), the
 128-query kernel from 256 (noncausal) or 512 (causal) groups of 128 queries, and
 otherwise the key-split kernel with 64-key tiles up to 256 query blocks of 32 and
-32-key tiles beyond. Each case below sits one step below or at a threshold; every
-row of the first and last head and sampled rows of the others are checked against the
-FP32 oracle (atol 2e-3 + rtol 1e-2).
+32-key tiles beyond. Each case below sits one step below or at a threshold, and
+`fa2_forward_plan` (the function the forward dispatches through) must name the kernel
+the case is meant to reach; every row of the first and last head and sampled rows of
+the others are checked against the FP32 oracle (atol 2e-3 + rtol 1e-2).
 """
 
 from __future__ import annotations
@@ -16,28 +17,30 @@ import pytest
 import torch
 
 import flash_attention_2_lab_amd as fa
+from flash_attention_2_lab_amd import capi
 from oracle import attention_rows_fp32
 
 pytestmark = pytest.mark.gpu
 
 ENTRY = fa.flash_attention_cuda.tensorcore_attention_forward_production_128x128
 
+K = capi
 CASES = [
-    # (batch, heads, seq_len, causal, kernel it runs)
-    (1, 127, 1024, False, "128-query (508 groups of 256)"),
-    (1, 128, 1024, False, "256-query (512 groups of 256)"),
-    (1, 31, 1024, False, "key-split, 32-key tiles (248 groups of 128)"),
-    (1, 32, 1024, False, "128-query (256 groups of 128)"),
-    (1, 8, 1024, False, "key-split, 64-key tiles (256 query blocks)"),
-    (1, 9, 1024, False, "key-split, 32-key tiles (288 query blocks)"),
-    (1, 255, 1024, True, "128-query (510 tile pairs)"),
-    (1, 256, 1024, True, "256-query, tile pairs (512 pairs)"),
-    (1, 409, 1280, True, "128-query (2045 single tiles, odd count per head)"),
-    (1, 410, 1280, True, "256-query, single tiles (2050, odd count per head)"),
-    (1, 63, 1024, True, "key-split, 32-key tiles (504 groups of 128)"),
-    (1, 64, 1024, True, "128-query (512 groups of 128)"),
-    (1, 8, 1024, True, "key-split, 64-key tiles (256 query blocks)"),
-    (3, 3, 1024, True, "key-split, 32-key tiles (288 query blocks)"),
+    # (batch, heads, seq_len, causal, kernel it runs, FA2_KERNEL_* id)
+    (1, 127, 1024, False, "128-query (508 groups of 256)", K.FA2_KERNEL_128_QUERY),
+    (1, 128, 1024, False, "256-query (512 groups of 256)", K.FA2_KERNEL_256_QUERY),
+    (1, 31, 1024, False, "key-split, 32-key tiles (248 groups of 128)", K.FA2_KERNEL_KEY_SPLIT_32),
+    (1, 32, 1024, False, "128-query (256 groups of 128)", K.FA2_KERNEL_128_QUERY),
+    (1, 8, 1024, False, "key-split, 64-key tiles (256 query blocks)", K.FA2_KERNEL_KEY_SPLIT_64),
+    (1, 9, 1024, False, "key-split, 32-key tiles (288 query blocks)", K.FA2_KERNEL_KEY_SPLIT_32),
+    (1, 255, 1024, True, "128-query (510 tile pairs)", K.FA2_KERNEL_128_QUERY),
+    (1, 256, 1024, True, "256-query, tile pairs (512 pairs)", K.FA2_KERNEL_256_QUERY_PAIRS),
+    (1, 409, 1280, True, "128-query (2045 single tiles, odd count per head)", K.FA2_KERNEL_128_QUERY),
+    (1, 410, 1280, True, "256-query, single tiles (2050, odd count per head)", K.FA2_KERNEL_256_QUERY),
+    (1, 63, 1024, True, "key-split, 32-key tiles (504 groups of 128)", K.FA2_KERNEL_KEY_SPLIT_32),
+    (1, 64, 1024, True, "128-query (512 groups of 128)", K.FA2_KERNEL_128_QUERY),
+    (1, 8, 1024, True, "key-split, 64-key tiles (256 query blocks)", K.FA2_KERNEL_KEY_SPLIT_64),
+    (3, 3, 1024, True, "key-split, 32-key tiles (288 query blocks)", K.FA2_KERNEL_KEY_SPLIT_32),
 ]
 
 
@@ -47,9 +50,10 @@ def _inputs(batch, heads, seq_len, seed):
     return tuple(torch.randn(shape, generator=gen).half() for _ in range(3))
 
 
-@pytest.mark.parametrize("batch, heads, seq_len, causal, kernel", CASES,
+@pytest.mark.parametrize("batch, heads, seq_len, causal, kernel, kernel_id", CASES,
                          ids=[("causal: " if c[3] else "noncausal: ") + c[4] for c in CASES])
-def test_threshold_shapes_match_oracle(batch, heads, seq_len, causal, kernel):
+def test_threshold_shapes_match_oracle(batch, heads, seq_len, causal, kernel, kernel_id):
+    assert capi.forward_plan(batch, heads, seq_len, causal) == kernel_id
     q, k, v = _inputs(batch, heads, seq_len, seed=31)
     out = ENTRY(q.cuda(), k.cuda(), v.cuda(), causal)
     torch.cuda.synchronize()

@@ -108,8 +108,21 @@ def extension_commands(object_file: Path) -> tuple[list[str], list[str]]:
     return compile_cmd, link_cmd
 
 
+C_CALLER_SOURCE = PACKAGE_DIR.parent / "tests" / "c_abi" / "caller.c"
+C_CALLER = C_CALLER_SOURCE.with_suffix("")
+
+
+def c_caller_command() -> list[str]:
+    """The plain C test caller of the C ABI (gcc, HIP runtime C API), linked to the
+    kernel library by $ORIGIN rpath."""
+    return ["gcc", "-std=c11", "-O2", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
+            f"-I{ROCM / 'include'}", f"-I{INCLUDE}", str(C_CALLER_SOURCE), "-o", str(C_CALLER),
+            f"-L{ROCM / 'lib'}", "-lamdhip64", f"-L{PACKAGE_DIR}", "-lfa2_mi355x",
+            "-Wl,-rpath,$ORIGIN/../../flash_attention_2_lab_amd", f"-Wl,-rpath,{ROCM / 'lib'}", "-lm"]
+
+
 def build(verbose: bool = False) -> None:
-    """Compile both libraries in place (always recompiles)."""
+    """Compile both libraries and the C test caller in place (always recompiles)."""
     BUILD_DIR.mkdir(exist_ok=True)
     object_file = BUILD_DIR / "flash_attention_cuda.o"
     compile_cmd, link_cmd = extension_commands(object_file)
@@ -120,6 +133,8 @@ def build(verbose: bool = False) -> None:
         for job in jobs:
             job.result()
     _run(link_cmd)
+    if C_CALLER_SOURCE.exists():
+        _run(c_caller_command())
     if verbose:
         print(f"built {KERNEL_LIBRARY.name} and {EXTENSION_LIBRARY.name} in {PACKAGE_DIR}")
 

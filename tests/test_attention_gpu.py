@@ -272,6 +272,29 @@ def test_runs_on_the_current_stream():
     assert torch.equal(via_c_abi, expected)
 
 
+def test_concurrent_streams_do_not_interfere():
+    # The forward keeps no state between calls (no scratch memory, no counters), so
+    # calls on different streams may overlap. Two side streams each run ten forwards
+    # of their own shape and inputs (256-query kernel, causal pairs; key-split kernel)
+    # at the same time; every output must equal the sequential result bitwise.
+    cases = [((8, 64, 1024), True, 51), ((1, 8, 1024), False, 52)]
+    inputs = [[t.cuda() for t in _inputs(*shape, seed=seed)] for shape, _, seed in cases]
+    expected = [ENTRY(*x, causal) for x, (_, causal, _) in zip(inputs, cases)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in cases]
+    outputs = [[], []]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    for _ in range(10):
+        for i, (s, x, (_, causal, _)) in enumerate(zip(streams, inputs, cases)):
+            with torch.cuda.stream(s):
+                outputs[i].append(ENTRY(*x, causal))
+    torch.cuda.synchronize()
+    for i in range(len(cases)):
+        for out in outputs[i]:
+            assert torch.equal(out, expected[i])
+
+
 @pytest.mark.parametrize("shape, causal", [((1, 8, 1024), False), ((1, 8, 1024), True),
                                            ((8, 16, 1024), False), ((8, 64, 1024), True)])
 def test_forward_replays_in_a_hip_graph(shape, causal):

@@ -35,6 +35,7 @@ FA2_KERNEL_256_QUERY_PAIRS = 2
 FA2_KERNEL_128_QUERY = 3
 FA2_KERNEL_KEY_SPLIT_64 = 4
 FA2_KERNEL_KEY_SPLIT_32 = 5
+FA2_KERNEL_KEY_SPLIT_8_WAVES = 6
 
 
 class Fa2Error(RuntimeError):

@@ -131,7 +131,8 @@ enum fa2_forward_kernel {
     FA2_KERNEL_128_QUERY = 3,        /* 128 queries per workgroup                          */
     FA2_KERNEL_KEY_SPLIT_64 = 4,     /* 32 queries per workgroup, keys split over 4 waves, */
                                      /* 64-key tiles                                       */
-    FA2_KERNEL_KEY_SPLIT_32 = 5      /* the same with 32-key tiles                         */
+    FA2_KERNEL_KEY_SPLIT_32 = 5,     /* the same with 32-key tiles                         */
+    FA2_KERNEL_KEY_SPLIT_8_WAVES = 6 /* keys split over 8 waves, 32-key tiles              */
 };
 
 /*

@@ -38,7 +38,8 @@ def test_status_codes_match_header():
 
 def test_kernel_ids_match_header():
     text = capi.HEADER_PATH.read_text()
-    for name in ("NONE", "256_QUERY", "256_QUERY_PAIRS", "128_QUERY", "KEY_SPLIT_64", "KEY_SPLIT_32"):
+    for name in ("NONE", "256_QUERY", "256_QUERY_PAIRS", "128_QUERY", "KEY_SPLIT_64", "KEY_SPLIT_32",
+                 "KEY_SPLIT_8_WAVES"):
         value = int(re.search(rf"FA2_KERNEL_{name} = (\d+)", text).group(1))
         assert getattr(capi, f"FA2_KERNEL_{name}") == value
 
@@ -60,6 +61,11 @@ K = capi
     (1, 410, 1280, True, K.FA2_KERNEL_256_QUERY), (1, 409, 1280, True, K.FA2_KERNEL_128_QUERY),
     (1, 64, 1024, True, K.FA2_KERNEL_128_QUERY), (1, 63, 1024, True, K.FA2_KERNEL_KEY_SPLIT_32),
     (1, 8, 1024, True, K.FA2_KERNEL_KEY_SPLIT_64),
+    # Key-split shapes from 2048 keys on split each block's keys over 8 waves.
+    (1, 2, 4096, False, K.FA2_KERNEL_KEY_SPLIT_8_WAVES), (1, 1, 2048, True, K.FA2_KERNEL_KEY_SPLIT_8_WAVES),
+    (1, 4, 2048, False, K.FA2_KERNEL_KEY_SPLIT_8_WAVES), (1, 1, 8192, True, K.FA2_KERNEL_KEY_SPLIT_8_WAVES),
+    (1, 4, 1024, False, K.FA2_KERNEL_KEY_SPLIT_64), (1, 8, 2048, True, K.FA2_KERNEL_KEY_SPLIT_32),
+    (1, 1, 2064, False, K.FA2_KERNEL_KEY_SPLIT_8_WAVES),
     # Sequence lengths the production entry rejects but the Bc16/Bc32 entries take
     # (partial last block) run the key-split kernel.
     (4, 64, 1040, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 2, 80, False, K.FA2_KERNEL_KEY_SPLIT_64),

@@ -4,8 +4,8 @@ The forward picks its kernel from (batch*heads, seq_len, causal) (fa2_forward.hi
 `forward`): the 256-query kernel from 512 workgroups (causal: pairs of query tiles
 when a head has an even number of them, else one tile per workgroup from 2048), the
 128-query kernel from 256 (noncausal) or 512 (causal) groups of 128 queries, and
-otherwise the key-split kernel with 64-key tiles up to 256 query blocks of 32 and
-32-key tiles beyond. Each case below sits one step below or at a threshold, and
+otherwise the key-split kernel: up to 256 query blocks of 32, 4 waves with 64-key tiles
+(8 waves with 32-key tiles from 2048 keys on), and 32-key tiles beyond. Each case below sits one step below or at a threshold, and
 `fa2_forward_plan` (the function the forward dispatches through) must name the kernel
 the case is meant to reach; every row of the first and last head and sampled rows of
 the others are checked against the FP32 oracle (atol 2e-3 + rtol 1e-2).
@@ -41,6 +41,10 @@ CASES = [
     (1, 64, 1024, True, "128-query (512 groups of 128)", K.FA2_KERNEL_128_QUERY),
     (1, 8, 1024, True, "key-split, 64-key tiles (256 query blocks)", K.FA2_KERNEL_KEY_SPLIT_64),
     (3, 3, 1024, True, "key-split, 32-key tiles (288 query blocks)", K.FA2_KERNEL_KEY_SPLIT_32),
+    (1, 4, 1024, False, "key-split, 64-key tiles (1024 keys)", K.FA2_KERNEL_KEY_SPLIT_64),
+    (1, 4, 2048, False, "key-split, 8 waves (2048 keys, 256 query blocks)", K.FA2_KERNEL_KEY_SPLIT_8_WAVES),
+    (1, 2, 4096, True, "key-split, 8 waves (4096 keys)", K.FA2_KERNEL_KEY_SPLIT_8_WAVES),
+    (1, 8, 2048, True, "key-split, 32-key tiles (512 query blocks of 2048 keys)", K.FA2_KERNEL_KEY_SPLIT_32),
 ]
 
 

@@ -76,6 +76,7 @@ def test_bc32_entries_reject_partial_key_tile(name):
     (1, 4, 16), (1, 4, 48), (1, 4, 80), (1, 4, 144), (2, 3, 208), (1, 8, 1040),
     (1, 4, 320),     # multiple of 64, not of 128: key-split kernel without partial tiles
     (4, 16, 2000),   # many workgroups, partial last tile
+    (1, 2, 2064),    # 8-wave key split, partial last tile
     (2, 32, 1024),   # multiple of 128 that fills the chip: the 128-query kernel
 ])
 def test_bc16_partial_tiles_match_oracle(batch, heads, seq_len):

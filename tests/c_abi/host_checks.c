@@ -1,0 +1,142 @@
+/*
+ * Host-side paths of the forward entry points of the C ABI (include/fa2_mi355x.h) that
+ * need no GPU: argument rejection, the empty problem, status strings and the kernel
+ * plan. Nothing here launches a kernel or calls the HIP runtime, so it runs on a
+ * machine without a GPU. The CPU test suite builds it with AddressSanitizer and
+ * UndefinedBehaviorSanitizer against a host-only sanitizer build of the library.
+ * Prints "ok" and exits 0 when every check passes.
+ */
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "fa2_mi355x.h"
+
+static int failures = 0;
+
+#define CHECK(cond, ...)                        \
+    do {                                        \
+        if (!(cond)) {                          \
+            fprintf(stderr, __VA_ARGS__);       \
+            fprintf(stderr, "\n");              \
+            ++failures;                         \
+        }                                       \
+    } while (0)
+
+/* Never dereferenced: every call below is rejected (or empty) before any launch. */
+static _Alignas(16) unsigned char fake[4][64];
+
+static int forward(const void* q, const void* k, const void* v, void* o, int64_t batch, int64_t heads,
+                   int64_t seq_len, int64_t head_dim, int causal) {
+    return fa2_forward_production_128x128(q, k, v, o, batch, heads, seq_len, head_dim, causal, NULL);
+}
+
+static int tensorcore(const void* q, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+                      int64_t key_tile) {
+    return fa2_forward_tensorcore(q, fake[1], fake[2], fake[3], batch, heads, seq_len, head_dim, key_tile, NULL);
+}
+
+int main(void) {
+    const void *q = fake[0], *k = fake[1], *v = fake[2];
+    void* o = fake[3];
+
+    CHECK(fa2_abi_version() == FA2_MI355X_ABI_VERSION, "ABI version %d", fa2_abi_version());
+
+    for (int causal = 0; causal <= 1; ++causal) {
+        /* Status precedence: negative sizes, head dim, sequence length, empty, null, alignment, size. */
+        CHECK(forward(q, k, v, o, -1, 1, 128, 64, causal) == FA2_STATUS_NEGATIVE_DIMENSION, "negative batch");
+        CHECK(forward(q, k, v, o, 1, -1, 128, 64, causal) == FA2_STATUS_NEGATIVE_DIMENSION, "negative heads");
+        CHECK(forward(q, k, v, o, 1, 1, -128, 64, causal) == FA2_STATUS_NEGATIVE_DIMENSION, "negative seq_len");
+        CHECK(forward(q, k, v, o, 1, 1, 128, -64, causal) == FA2_STATUS_NEGATIVE_DIMENSION, "negative head_dim");
+        CHECK(forward(q, k, v, o, 1, 1, 128, 32, causal) == FA2_STATUS_BAD_HEAD_DIM, "head_dim 32");
+        CHECK(forward(q, k, v, o, 1, 1, 128, 128, causal) == FA2_STATUS_BAD_HEAD_DIM, "head_dim 128");
+        CHECK(forward(NULL, NULL, NULL, NULL, 0, 1, 128, 32, causal) == FA2_STATUS_BAD_HEAD_DIM,
+              "empty problem still checks head_dim");
+        for (int64_t n = 1; n < 128; n += 17)
+            CHECK(forward(q, k, v, o, 1, 1, n, 64, causal) == FA2_STATUS_BAD_SEQUENCE_LENGTH, "seq_len %lld",
+                  (long long)n);
+        CHECK(forward(q, k, v, o, 1, 1, 200, 64, causal) == FA2_STATUS_BAD_SEQUENCE_LENGTH, "seq_len 200");
+        CHECK(forward(NULL, NULL, NULL, NULL, 0, 8, 1024, 64, causal) == FA2_STATUS_SUCCESS, "empty batch");
+        CHECK(forward(NULL, NULL, NULL, NULL, 2, 0, 1024, 64, causal) == FA2_STATUS_SUCCESS, "empty heads");
+        CHECK(forward(NULL, NULL, NULL, NULL, 2, 8, 0, 64, causal) == FA2_STATUS_SUCCESS, "empty sequence");
+        CHECK(forward(NULL, k, v, o, 1, 1, 128, 64, causal) == FA2_STATUS_NULL_POINTER, "null query");
+        CHECK(forward(q, NULL, v, o, 1, 1, 128, 64, causal) == FA2_STATUS_NULL_POINTER, "null key");
+        CHECK(forward(q, k, NULL, o, 1, 1, 128, 64, causal) == FA2_STATUS_NULL_POINTER, "null value");
+        CHECK(forward(q, k, v, NULL, 1, 1, 128, 64, causal) == FA2_STATUS_NULL_POINTER, "null output");
+        for (int shift = 1; shift < 16; ++shift) {
+            const unsigned char* bad = fake[0] + shift;
+            CHECK(forward(bad, k, v, o, 1, 1, 128, 64, causal) == FA2_STATUS_MISALIGNED, "query + %d", shift);
+            CHECK(forward(q, bad, v, o, 1, 1, 128, 64, causal) == FA2_STATUS_MISALIGNED, "key + %d", shift);
+            CHECK(forward(q, k, bad, o, 1, 1, 128, 64, causal) == FA2_STATUS_MISALIGNED, "value + %d", shift);
+            CHECK(forward(q, k, v, (void*)bad, 1, 1, 128, 64, causal) == FA2_STATUS_MISALIGNED, "output + %d", shift);
+        }
+        /* Beyond the 32-bit slab offsets and the 1-D grid; products near INT64_MAX must not overflow. */
+        CHECK(forward(q, k, v, o, 1, 1, ((int64_t)1 << 24) + 128, 64, causal) == FA2_STATUS_TOO_LARGE, "seq_len 2^24+128");
+        CHECK(forward(q, k, v, o, (int64_t)1 << 40, (int64_t)1 << 40, 128, 64, causal) == FA2_STATUS_TOO_LARGE,
+              "batch * heads beyond int64");
+        CHECK(forward(q, k, v, o, INT64_MAX, 1, 128, 64, causal) == FA2_STATUS_TOO_LARGE, "batch INT64_MAX");
+        CHECK(forward(q, k, v, o, 1, INT64_MAX, 128, 64, causal) == FA2_STATUS_TOO_LARGE, "heads INT64_MAX");
+        CHECK(forward(q, k, v, o, (int64_t)1 << 31, 1 << 12, 1 << 12, 64, causal) == FA2_STATUS_TOO_LARGE,
+              "grid beyond 2^32 groups");
+        CHECK(forward(q, k, v, o, INT64_MAX, INT64_MAX, INT64_MAX, 64, causal) == FA2_STATUS_BAD_SEQUENCE_LENGTH,
+              "INT64_MAX sizes");
+    }
+
+    /* fa2_forward_tensorcore: key tile 16 or 32, seq_len a multiple of it, same other checks.
+     * The key tile is checked first; a null query stops an accepted tile before any launch. */
+    for (int64_t tile = -1; tile <= 64; ++tile) {
+        const int status = tensorcore(NULL, 1, 1, 64, 64, tile);
+        if (tile == 16 || tile == 32)
+            CHECK(status == FA2_STATUS_NULL_POINTER, "key tile %lld: status %d", (long long)tile, status);
+        else
+            CHECK(status == FA2_STATUS_BAD_KEY_TILE, "key tile %lld: status %d", (long long)tile, status);
+    }
+    CHECK(tensorcore(q, 1, 1, 48, 64, 32) == FA2_STATUS_BAD_SEQUENCE_LENGTH, "48 keys, tile 32");
+    CHECK(tensorcore(q, 1, 1, 40, 64, 16) == FA2_STATUS_BAD_SEQUENCE_LENGTH, "40 keys, tile 16");
+    CHECK(tensorcore(q, 1, 1, 48, 32, 16) == FA2_STATUS_BAD_HEAD_DIM, "tensorcore head_dim");
+    CHECK(tensorcore(NULL, 1, 1, 48, 64, 16) == FA2_STATUS_NULL_POINTER, "tensorcore null query");
+    CHECK(tensorcore(fake[0] + 8, 1, 1, 48, 64, 16) == FA2_STATUS_MISALIGNED, "tensorcore misaligned query");
+    CHECK(tensorcore(NULL, 0, 1, 48, 64, 16) == FA2_STATUS_SUCCESS, "tensorcore empty batch");
+
+    /* Every status has a text; unknown codes have one too (static storage, never NULL). */
+    const int codes[] = {FA2_STATUS_SUCCESS, FA2_STATUS_NULL_POINTER, FA2_STATUS_NEGATIVE_DIMENSION,
+                         FA2_STATUS_BAD_HEAD_DIM, FA2_STATUS_BAD_SEQUENCE_LENGTH, FA2_STATUS_MISALIGNED,
+                         FA2_STATUS_TOO_LARGE, FA2_STATUS_BAD_KEY_TILE, FA2_STATUS_HIP_ERROR_BASE + 1,
+                         FA2_STATUS_HIP_ERROR_BASE + 98, -1, 8, 999, INT32_MAX, INT32_MIN};
+    for (size_t i = 0; i < sizeof(codes) / sizeof(codes[0]); ++i) {
+        const char* text = fa2_status_string(codes[i]);
+        CHECK(text != NULL && strlen(text) > 0, "status %d has no text", codes[i]);
+    }
+    CHECK(strcmp(fa2_status_string(FA2_STATUS_BAD_HEAD_DIM), "head dimension must equal 64") == 0, "head dim text");
+
+    /* The plan is a pure function of the sizes, defined for every input: NONE for empty or
+     * negative sizes, seq_len > 2^24 and grids beyond 2^32 32-query blocks; a kernel
+     * otherwise (the plan does not check the entry's seq_len multiple). */
+    const int64_t sizes[] = {-1, 0, 1, 16, 17, 32, 48, 64, 96, 128, 200, 256, 384, 512, 768, 1024, 1040,
+                             2048, 4096, 8192, 16384, (int64_t)1 << 24, ((int64_t)1 << 24) + 256, INT64_MAX};
+    const int64_t counts[] = {-1, 0, 1, 2, 3, 8, 16, 32, 64, 256, 4096, (int64_t)1 << 31, INT64_MAX};
+    const size_t ns = sizeof(sizes) / sizeof(sizes[0]), nc = sizeof(counts) / sizeof(counts[0]);
+    for (size_t a = 0; a < nc; ++a)
+        for (size_t b = 0; b < nc; ++b)
+            for (size_t c = 0; c < ns; ++c)
+                for (int causal = 0; causal <= 1; ++causal) {
+                    const int64_t batch = counts[a], heads = counts[b], n = sizes[c];
+                    const int plan = fa2_forward_plan(batch, heads, n, causal);
+                    CHECK(plan >= FA2_KERNEL_NONE && plan <= FA2_KERNEL_KEY_SPLIT_8_WAVES, "plan %d", plan);
+                    int none = batch <= 0 || heads <= 0 || n <= 0 || n > ((int64_t)1 << 24);
+                    if (!none) none = batch > (int64_t)UINT32_MAX / heads;
+                    if (!none) none = batch * heads > (int64_t)UINT32_MAX / ((n + 31) / 32);
+                    CHECK((plan == FA2_KERNEL_NONE) == none, "plan %d for %lld %lld %lld causal=%d", plan,
+                          (long long)batch, (long long)heads, (long long)n, causal);
+                }
+    CHECK(fa2_forward_plan(1, 8, 1024, 0) == FA2_KERNEL_KEY_SPLIT_64, "plan bench size");
+    CHECK(fa2_forward_plan(16, 16, 4096, 0) == FA2_KERNEL_256_QUERY, "plan throughput size");
+    CHECK(fa2_forward_plan(16, 16, 4096, 1) == FA2_KERNEL_256_QUERY_PAIRS, "plan throughput size causal");
+
+    if (failures) {
+        fprintf(stderr, "%d check(s) failed\n", failures);
+        return 1;
+    }
+    printf("ok\n");
+    return 0;
+}

@@ -59,7 +59,7 @@ constexpr float kRescaleLog2 = 14.0f;                     // lazy-rescale thresh
 // 2 * 2^14 = 2^15 < 65504.
 constexpr float kTileSumBound = 16384.0f;                 // 2^kRescaleLog2
 static_assert(kTileSumBound == 16384.0f && kRescaleLog2 == 14.0f, "kTileSumBound is 2^kRescaleLog2");
-constexpr int64_t kMaxSeqLen = (int64_t)1 << 24;          // seq_len * 128 B fits in int32
+constexpr int64_t kMaxSeqLen = (int64_t)1 << 24;          // byte offsets in a head's slab fit in int32
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
@@ -119,8 +119,9 @@ __device__ __forceinline__ f16x4 lds_read_transposed(const uint8_t* p) {
 // Buffer loads take the slab base from SGPRs and a 32-bit per-lane offset, and
 // return zeros outside num_records instead of faulting.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t head_resource(const void* base, int seq_len) {
+    // num_records = seq_len * 128 reaches 2^31 at the largest seq_len: unsigned arithmetic.
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
-                                            seq_len * kRowBytes, 0x00020000);
+                                            (int)((uint32_t)seq_len * (uint32_t)kRowBytes), 0x00020000);
 }
 
 // One LDS-DMA instruction (buffer_load_dwordx4 ... lds) moves 1 KiB: rows r0..r0+7
@@ -570,7 +571,7 @@ __device__ __forceinline__ u32x4 head_descriptor(const void* base, int seq_len) 
     u32x4 d;
     d[0] = __builtin_amdgcn_readfirstlane((uint32_t)a);
     d[1] = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu);
-    d[2] = (uint32_t)(seq_len * kRowBytes);
+    d[2] = (uint32_t)seq_len * (uint32_t)kRowBytes;  // up to 2^31: unsigned arithmetic
     d[3] = 0x00020000u;
     return d;
 }

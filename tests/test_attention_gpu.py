@@ -177,6 +177,26 @@ def test_long_context_b2_h32_n16384_sigma2_causal():
 
 
 @pytest.mark.parametrize("causal", [False, True])
+def test_long_single_head_n2pow20(causal):
+    # One head of 2^20 keys: 128 MiB per tensor, byte offsets up to 2^27 inside the slab
+    # and 16384 key tiles streamed by each workgroup (the 256-query kernel, as pairs of
+    # query tiles when causal).
+    seq_len = 1 << 20
+    expected_kernel = capi.FA2_KERNEL_256_QUERY_PAIRS if causal else capi.FA2_KERNEL_256_QUERY
+    assert capi.forward_plan(1, 1, seq_len, causal) == expected_kernel
+    q, k, v = _inputs(1, 1, seq_len, seed=21)
+    out = _run(q, k, v, causal).cpu()
+    assert torch.isfinite(out).all()
+    rows = _sample_rows(1, 1, seq_len, 96, seed=22)
+    rows = sorted(set(rows) | {(0, 0, seq_len - 256), (0, 0, seq_len - 257), (0, 0, seq_len // 2)})
+    expected = attention_rows_fp32(q, k, v, rows, causal=causal)
+    actual = torch.stack([out[b, h, i] for b, h, i in rows])
+    _assert_close_to_oracle(actual, expected)
+    if causal:
+        assert torch.equal(out[:, :, 0], v[:, :, 0])
+
+
+@pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("shape", [(1, 64, 1024), (1, 8, 1024)])
 def test_growing_scores_match_oracle(shape, causal):
     # Key norms ramp up 12x along the sequence, so the running max keeps growing (by

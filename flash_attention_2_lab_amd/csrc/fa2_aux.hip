@@ -48,7 +48,7 @@ __global__ __launch_bounds__(256) void copy_kernel(const T* __restrict__ src, T*
 template <typename T>
 hipError_t launch_copy(const void* src, void* dst, int64_t bytes, hipStream_t stream) {
     const int64_t count = bytes / (int64_t)sizeof(T);
-    const int64_t blocks = (count + 255) / 256;
+    const int64_t blocks = count / 256 + (count % 256 != 0);
     const unsigned grid = (unsigned)(blocks < 65536 ? blocks : 65536);
     hipLaunchKernelGGL((copy_kernel<T>), dim3(grid), dim3(256), 0, stream, static_cast<const T*>(src),
                        static_cast<T*>(dst), count);
@@ -262,9 +262,9 @@ extern "C" int fa2_attention_scores_f32(const float* query, const float* key, fl
     if (batch_heads == 0 || seq_len == 0) return FA2_STATUS_SUCCESS;
     if (!query || !key || !scores) return FA2_STATUS_NULL_POINTER;
     if (!aligned_to(query, 4) || !aligned_to(key, 4) || !aligned_to(scores, 4)) return FA2_STATUS_MISALIGNED;
-    const int64_t tiles = (seq_len + kScoreTile - 1) / kScoreTile;
-    if (seq_len > INT32_MAX || head_dim > INT32_MAX || batch_heads > (int64_t)UINT32_MAX / (tiles * tiles))
-        return FA2_STATUS_TOO_LARGE;
+    if (seq_len > INT32_MAX || head_dim > INT32_MAX) return FA2_STATUS_TOO_LARGE;
+    const int64_t tiles = (seq_len + kScoreTile - 1) / kScoreTile;  // seq_len <= INT32_MAX: no overflow
+    if (batch_heads > (int64_t)UINT32_MAX / (tiles * tiles)) return FA2_STATUS_TOO_LARGE;
     // scale = 1/sqrt(head_dim) in FP32, as the reference's host code computes it
     // (head_dim 0 gives +inf and scores of 0 * inf = NaN there too).
     const float scale = 1.0f / sqrtf((float)head_dim);
@@ -283,8 +283,9 @@ extern "C" int fa2_attention_forward_f32(const float* query, const float* key, c
     if (!query || !key || !value || !output) return FA2_STATUS_NULL_POINTER;
     if (!aligned_to(query, 4) || !aligned_to(key, 4) || !aligned_to(value, 4) || !aligned_to(output, 4))
         return FA2_STATUS_MISALIGNED;
-    const int64_t tiles = (seq_len + kF32Queries - 1) / kF32Queries;
-    if (seq_len > INT32_MAX || batch_heads > (int64_t)UINT32_MAX / tiles) return FA2_STATUS_TOO_LARGE;
+    if (seq_len > INT32_MAX) return FA2_STATUS_TOO_LARGE;
+    const int64_t tiles = (seq_len + kF32Queries - 1) / kF32Queries;  // seq_len <= INT32_MAX: no overflow
+    if (batch_heads > (int64_t)UINT32_MAX / tiles) return FA2_STATUS_TOO_LARGE;
     const float scale_log2 = 1.0f / sqrtf((float)head_dim) * 1.4426950408889634074f;
     const dim3 grid((unsigned)(batch_heads * tiles));
     hipStream_t s = static_cast<hipStream_t>(stream);

@@ -1,6 +1,6 @@
 /*
- * Host-side paths of the forward entry points of the C ABI (include/fa2_mi355x.h) that
- * need no GPU: argument rejection, the empty problem, status strings and the kernel
+ * Host-side paths of the C ABI (include/fa2_mi355x.h) that need no GPU: argument
+ * rejection and empty problems of every entry point, status strings and the kernel
  * plan. Nothing here launches a kernel or calls the HIP runtime, so it runs on a
  * machine without a GPU. The CPU test suite builds it with AddressSanitizer and
  * UndefinedBehaviorSanitizer against a host-only sanitizer build of the library.
@@ -129,6 +129,47 @@ int main(void) {
                     CHECK((plan == FA2_KERNEL_NONE) == none, "plan %d for %lld %lld %lld causal=%d", plan,
                           (long long)batch, (long long)heads, (long long)n, causal);
                 }
+    /* The module's other entry points: rejected and empty calls only (valid sizes would launch). */
+    const float* fq = (const float*)fake[0];
+    float* fo = (float*)fake[3];
+    CHECK(fa2_copy(fake[0], fake[1], -1, NULL) == FA2_STATUS_NEGATIVE_DIMENSION, "copy negative");
+    CHECK(fa2_copy(NULL, NULL, 0, NULL) == FA2_STATUS_SUCCESS, "copy empty");
+    CHECK(fa2_copy(NULL, fake[1], 16, NULL) == FA2_STATUS_NULL_POINTER, "copy null source");
+    CHECK(fa2_copy(fake[0], NULL, 16, NULL) == FA2_STATUS_NULL_POINTER, "copy null destination");
+    {
+        /* Lengths beyond int32 and counts beyond the 2^32-workgroup grid: rejected whatever
+         * the other sizes (a count that fits the grid would launch). */
+        const int64_t long_len[] = {(int64_t)INT32_MAX + 1, INT64_MAX - 1, INT64_MAX};
+        const int64_t big_count[] = {(int64_t)UINT32_MAX + 1, INT64_MAX - 1, INT64_MAX};
+        for (size_t i = 0; i < 3; ++i) {
+            CHECK(fa2_attention_scores_f32(fq, fq, fo, 1, long_len[i], 64, NULL) == FA2_STATUS_TOO_LARGE,
+                  "scores seq_len %lld", (long long)long_len[i]);
+            CHECK(fa2_attention_scores_f32(fq, fq, fo, 1, 64, long_len[i], NULL) == FA2_STATUS_TOO_LARGE,
+                  "scores head_dim %lld", (long long)long_len[i]);
+            CHECK(fa2_attention_scores_f32(fq, fq, fo, big_count[i], 64, 64, NULL) == FA2_STATUS_TOO_LARGE,
+                  "scores batch_heads %lld", (long long)big_count[i]);
+            CHECK(fa2_attention_forward_f32(fq, fq, fq, fo, 1, long_len[i], 64, NULL) == FA2_STATUS_TOO_LARGE,
+                  "f32 forward seq_len %lld", (long long)long_len[i]);
+            CHECK(fa2_attention_forward_f32(fq, fq, fq, fo, big_count[i], 64, 128, NULL) == FA2_STATUS_TOO_LARGE,
+                  "f32 forward batch_heads %lld", (long long)big_count[i]);
+            CHECK(fa2_matmul_16x64x16_f16(fake[0], fake[1], fo, big_count[i], NULL) == FA2_STATUS_TOO_LARGE,
+                  "matmul batch %lld", (long long)big_count[i]);
+        }
+    }
+    CHECK(fa2_attention_scores_f32(fq, fq, fo, -1, 64, 64, NULL) == FA2_STATUS_NEGATIVE_DIMENSION, "scores negative");
+    CHECK(fa2_attention_scores_f32(NULL, NULL, NULL, 0, 64, 64, NULL) == FA2_STATUS_SUCCESS, "scores empty");
+    CHECK(fa2_attention_scores_f32(NULL, fq, fo, 1, 64, 64, NULL) == FA2_STATUS_NULL_POINTER, "scores null");
+    CHECK(fa2_attention_scores_f32((const float*)(fake[0] + 2), fq, fo, 1, 64, 64, NULL) == FA2_STATUS_MISALIGNED,
+          "scores misaligned");
+    CHECK(fa2_attention_forward_f32(fq, fq, fq, fo, 1, 64, 96, NULL) == FA2_STATUS_BAD_HEAD_DIM, "f32 head_dim 96");
+    CHECK(fa2_attention_forward_f32(fq, fq, fq, fo, 1, -1, 64, NULL) == FA2_STATUS_NEGATIVE_DIMENSION, "f32 negative");
+    CHECK(fa2_attention_forward_f32(NULL, NULL, NULL, NULL, 1, 0, 64, NULL) == FA2_STATUS_SUCCESS, "f32 empty");
+    CHECK(fa2_attention_forward_f32(fq, fq, NULL, fo, 1, 64, 64, NULL) == FA2_STATUS_NULL_POINTER, "f32 null value");
+    CHECK(fa2_matmul_16x64x16_f16(fake[0], fake[1], fo, -1, NULL) == FA2_STATUS_NEGATIVE_DIMENSION, "matmul negative");
+    CHECK(fa2_matmul_16x64x16_f16(NULL, NULL, NULL, 0, NULL) == FA2_STATUS_SUCCESS, "matmul empty");
+    CHECK(fa2_matmul_16x64x16_f16(fake[0], NULL, fo, 1, NULL) == FA2_STATUS_NULL_POINTER, "matmul null");
+    CHECK(fa2_matmul_16x64x16_f16(fake[0] + 1, fake[1], fo, 1, NULL) == FA2_STATUS_MISALIGNED, "matmul misaligned");
+
     CHECK(fa2_forward_plan(1, 8, 1024, 0) == FA2_KERNEL_KEY_SPLIT_64, "plan bench size");
     CHECK(fa2_forward_plan(16, 16, 4096, 0) == FA2_KERNEL_256_QUERY, "plan throughput size");
     CHECK(fa2_forward_plan(16, 16, 4096, 1) == FA2_KERNEL_256_QUERY_PAIRS, "plan throughput size causal");

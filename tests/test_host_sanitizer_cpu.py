@@ -1,9 +1,9 @@
 """The C ABI's host-side paths under AddressSanitizer and UndefinedBehaviorSanitizer.
 
-`tests/c_abi/host_checks.c` calls the forward entry points only with arguments they
-reject (or with an empty problem), plus `fa2_status_string` and `fa2_forward_plan`, so
-nothing is launched and no GPU is needed. The library is rebuilt here from
-`fa2_forward.hip` with the sanitizers on its host code only (`-Xarch_host`), and the
+`tests/c_abi/host_checks.c` calls every entry point only with arguments it rejects (or
+with an empty problem), plus `fa2_status_string` and `fa2_forward_plan`, so nothing is
+launched and no GPU is needed. The library is rebuilt here from `fa2_forward.hip` and
+`fa2_aux.hip` with the sanitizers on their host code only (`-Xarch_host`), and the
 checker is built by clang so that both use clang's sanitizer runtime. Any sanitizer
 report aborts the run (`-fno-sanitize-recover=all`).
 """
@@ -20,7 +20,8 @@ REPO_ROOT = Path(__file__).resolve().parents[1]
 ROCM = Path("/opt/rocm")
 HIPCC = ROCM / "bin" / "hipcc"
 CLANG = ROCM / "llvm" / "bin" / "clang"
-SOURCE = REPO_ROOT / "flash_attention_2_lab_amd" / "csrc" / "fa2_forward.hip"
+CSRC = REPO_ROOT / "flash_attention_2_lab_amd" / "csrc"
+SOURCES = [CSRC / "fa2_forward.hip", CSRC / "fa2_aux.hip"]
 CHECKS = REPO_ROOT / "tests" / "c_abi" / "host_checks.c"
 INCLUDE = REPO_ROOT / "include"
 SANITIZE = ["-fsanitize=address", "-fsanitize=undefined", "-fno-sanitize-recover=all",
@@ -37,7 +38,7 @@ def test_host_paths_are_clean_under_sanitizers(tmp_path: Path) -> None:
     host_flags = [flag for option in SANITIZE for flag in ("-Xarch_host", option)]
     build = _run([str(HIPCC), "--offload-arch=gfx950", "-O1", "-g", "-std=c++17", "-fPIC", "-shared",
                   "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", *host_flags,
-                  f"-I{INCLUDE}", str(SOURCE), "-o", str(library)])
+                  f"-I{INCLUDE}", *(str(p) for p in SOURCES), "-o", str(library)])
     assert build.returncode == 0, build.stdout + build.stderr
 
     checker = tmp_path / "host_checks"

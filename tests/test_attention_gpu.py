@@ -113,8 +113,9 @@ def test_golden_vectors_through_binding_and_c_abi():
 
 def _sample_rows(batch, heads, seq_len, count, seed):
     gen = torch.Generator().manual_seed(seed)
-    rows = {(0, 0, 0), (0, 0, 1), (batch - 1, heads - 1, seq_len - 1), (0, heads - 1, 127),
-            (batch - 1, 0, 128), (0, 0, 63), (0, 0, 64)}
+    fixed = {(0, 0, 0), (0, 0, 1), (batch - 1, heads - 1, seq_len - 1), (0, heads - 1, 127),
+             (batch - 1, 0, 128), (0, 0, 63), (0, 0, 64)}
+    rows = {r for r in fixed if r[2] < seq_len}
     while len(rows) < count:
         b = int(torch.randint(batch, (1,), generator=gen))
         h = int(torch.randint(heads, (1,), generator=gen))
@@ -174,6 +175,33 @@ def test_long_context_b2_h32_n16384_sigma2_causal():
     actual = torch.stack([out[b, h, i] for b, h, i in rows])
     _assert_close_to_oracle(actual, expected)
     assert torch.equal(out[:, :, 0], v[:, :, 0])
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_maximum_reference_grid(causal):
+    # batch*heads = 65535, the largest the reference's launcher accepts: 65535 workgroups of
+    # the 128-query kernel, 7 more than a multiple of the 8-XCD remap, 1 GiB per tensor.
+    # Inputs are drawn on the device; the oracle reads the sampled heads back.
+    batch, heads, seq_len = 65535, 1, 128
+    assert capi.forward_plan(batch, heads, seq_len, causal) == capi.FA2_KERNEL_128_QUERY
+    gen = torch.Generator(device="cuda").manual_seed(31)
+    shape = (batch, heads, seq_len, 64)
+    q, k, v = (torch.randn(shape, generator=gen, device="cuda", dtype=torch.float16) for _ in range(3))
+    out = ENTRY(q, k, v, causal)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    rows = _sample_rows(batch, heads, seq_len, 64, seed=32)
+    rows = sorted(set(rows) | {(b, 0, i) for b in (0, 1, 7, 8, 8191, 8192, 65527, 65534) for i in (0, 127)})
+    assert all(b < batch and h < heads and i < seq_len for b, h, i in rows)
+    # The oracle runs on CPU copies of the sampled batch entries only.
+    picked = sorted({b for b, _, _ in rows})
+    where = {b: n for n, b in enumerate(picked)}
+    index = torch.tensor(picked, device="cuda")
+    q_s, k_s, v_s = (t.index_select(0, index).cpu() for t in (q, k, v))
+    expected = attention_rows_fp32(q_s, k_s, v_s, [(where[b], h, i) for b, h, i in rows], causal=causal)
+    out_s = out.index_select(0, index).cpu()
+    actual = torch.stack([out_s[where[b], h, i] for b, h, i in rows])
+    _assert_close_to_oracle(actual, expected)
 
 
 @pytest.mark.parametrize("causal", [False, True])

@@ -45,6 +45,8 @@ CASES = [
     (1, 4, 2048, False, "key-split, 8 waves (2048 keys, 256 query blocks)", K.FA2_KERNEL_KEY_SPLIT_8_WAVES),
     (1, 2, 4096, True, "key-split, 8 waves (4096 keys)", K.FA2_KERNEL_KEY_SPLIT_8_WAVES),
     (1, 8, 2048, True, "key-split, 32-key tiles (512 query blocks of 2048 keys)", K.FA2_KERNEL_KEY_SPLIT_32),
+    (2, 256, 256, False, "256-query (512 groups, the shortest key stream: 4 tiles)", K.FA2_KERNEL_256_QUERY),
+    (8, 256, 256, True, "256-query, single tiles (2048 heads of one query tile)", K.FA2_KERNEL_256_QUERY),
 ]
 
 

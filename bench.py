@@ -299,7 +299,7 @@ def main() -> int:
         f = attention_flops(2, 32, 16384, 64, True)
         north["B2H32N16384_causal_sigma2"] = {"us": round(t["causal"] * 1e6, 2),
                                               "tflops": round(f / t["causal"] / 1e12, 2),
-                                              "roofline": roofline(f, t["causal"])}
+                                              "roofline": roofline(f, t["causal"], "b2h32n16384/causal")}
         del long_ctx
         line["north_star"] = north
 

@@ -602,7 +602,9 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_splitk_kernel(const _
     constexpr int kDmaPerMatrix = kTileBytesW / 1024;        // 1 KiB = 8 rows per instruction
     constexpr int kDmaPerTile = 2 * kDmaPerMatrix;           // one wave fetches whole tiles
     constexpr int kMergeBytes = kSplit * (8 * 64 * 16 + 2 * 64 * 4);
-    constexpr int kSmemBytes = kSplit * 2 * kStageBytes > kMergeBytes ? kSplit * 2 * kStageBytes : kMergeBytes;
+    constexpr int kQBytes = kQueriesPerWave * kRowBytes;  // the block's Q rows, 4 KiB per wave
+    constexpr int kWaveBytes = 2 * kStageBytes + kQBytes;
+    constexpr int kSmemBytes = kSplit * kWaveBytes > kMergeBytes ? kSplit * kWaveBytes : kMergeBytes;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmemBytes];
 
     const int tid = threadIdx.x;
@@ -637,7 +639,7 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_splitk_kernel(const _
     const int t_begin = wave * visible_tiles / kSplit;
     const int t_end = (wave + 1) * visible_tiles / kSplit;
 
-    uint8_t* const my_stages = smem + wave * 2 * kStageBytes;
+    uint8_t* const my_stages = smem + wave * kWaveBytes;
     const uint32_t my_stages_addr = lds_address(my_stages);
     const int dma_off[2] = {dma_lane_offset(lane, 0), dma_lane_offset(lane, 1)};
     auto dma_tile = [&](int t, int st) {
@@ -654,15 +656,24 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_splitk_kernel(const _
         }
     };
 
-    // Lanes past the last query (partial block) score a zero query; their output
-    // is not stored.
-    f16x8 q_frag[4];
+    // Q rows of the block go to this wave's LDS area by LDS-DMA ahead of the first key
+    // tile, so the first tile's wait covers them; the fragments are read from LDS after
+    // it. (Loads into registers would make the compiler wait for them with a vmcnt that
+    // also counts the key-tile DMAs issued after them.) Rows past seq_len read as zeros,
+    // so lanes past the last query (partial block) score a zero query.
+    const u32x4 q_desc = head_descriptor(q_head, seq_len);
+    uint8_t* const my_q = my_stages + 2 * kStageBytes;
+    const uint32_t my_q_addr = my_stages_addr + 2 * kStageBytes;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-        q_frag[ks] = query_valid ? *reinterpret_cast<const f16x8*>(q_head + (size_t)my_query * kHeadDim +
-                                                                   ks * 16 + half * 8)
-                                 : f16x8{};
+    for (int n = 0; n < kQBytes / 1024; ++n) {
+        const int r0 = n * 8;
+        const int src = (q0 + r0) * kRowBytes;
+        if (kPartial) dma16_asm_checked(q_desc, my_q_addr + (uint32_t)(r0 * kRowBytes), dma_off[n & 1] + src);
+        else dma16_asm(q_desc, my_q_addr + (uint32_t)(r0 * kRowBytes), dma_off[n & 1], src);
+    }
     if (t_begin < t_end) dma_tile(t_begin, 0);
+    const int q_swz = tile_swizzle(lq);
+    f16x8 q_frag[4];
 
     const int k_row = key_of_mfma_row(lq);
     const int k_swz = tile_swizzle(k_row);
@@ -744,6 +755,11 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_splitk_kernel(const _
         }
         const uint8_t* k_lds = my_stages + st * kStageBytes;
         const uint8_t* v_lds = k_lds + kTileBytesW;
+        if (t == t_begin) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                q_frag[ks] = *reinterpret_cast<const f16x8*>(my_q + lq * kRowBytes + (((2 * ks + half) ^ q_swz) << 4));
+        }
 
         // S^T = K Q^T for the tile's 32-key blocks.
         f16x8 kf[kBlocks][4];
@@ -800,7 +816,9 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_splitk_kernel(const _
         }
     }
 
-    // Merge the partial results (stages are free once every wave is done).
+    // Merge the partial results (stages are free once every wave is done). A wave without
+    // key tiles still has its Q DMA to wait for before the merge reuses that LDS.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     float* red_o = reinterpret_cast<float*>(smem);                  // [wave][8][64 lanes][4]
     float* red_m = red_o + kSplit * 8 * 64 * 4;                      // [wave][64]

@@ -6,21 +6,22 @@ one noncausal forward plus one causal forward through the product entry point
 `flash_attention_cuda.tensorcore_attention_forward_production_128x128`, on
 synthetic inputs already resident in HBM.
 
-Inside the timed region the K steps run as K back-to-back noncausal calls followed
-by K back-to-back causal calls (the same work as K interleaved steps), with HIP
-events on the launch stream at the start, between the two batches and at the
-end - the reference harness's method (benchmarks/harness.py:34-71: events around
-back-to-back calls). Those events give each kernel's average launch duration for
-the `roofline` object; wall-clock time between two device synchronisations gives
-`ms_per_step`.
+Inside the timed region the K steps run as four batches of back-to-back calls in
+mirrored order - K/2 noncausal, K/2 causal, the other K/2 causal, the other K/2
+noncausal (the same work as K interleaved steps, with neither mode always first) -
+with HIP events on the launch stream between the batches: the reference harness's
+method (benchmarks/harness.py:34-71: events around back-to-back calls). Those events
+give each kernel's average launch duration for the `roofline` object; wall-clock time
+between two device synchronisations gives `ms_per_step`.
 
 Also reported (extra keys, each timed the same way after the main region):
 `north_star` - B16 H16 N4096 noncausal and causal (the >=50%-of-MFMA-peak target)
 and B2 H32 N16384 causal with sigma=2 logits; `cpu_baseline` - the oracle's FP32
 CPU restatement of the reference (oracle.attention_reference) timed on this host's
-cores on a bounded sample of the same workload; `graph_us` - the same K calls per
-mode captured once in a HIP graph and replayed (per-call time, median of three
-replays), for callers that capture launch-bound loops.
+cores (os.cpu_count() torch threads) on a bounded sample of the same workload, with
+the other BASELINE configurations' CPU rates under `configs`; `graph_us` - the same
+K calls per mode captured once in a HIP graph and replayed (per-call time, median of
+three replays), for callers that capture launch-bound loops.
 
 FLOPs: 4*B*H*N^2*D per forward, halved for causal. Bytes: 8*B*H*N*D (read Q, K, V
 and write O once, FP16).
@@ -65,28 +66,36 @@ def make_inputs(batch, heads, seq_len, *, seed=0, sigma=1.0, device="cpu"):
 
 
 def time_kernel_batches(entry, inputs, modes, steps, warmup):
-    """Runs `warmup` untimed rounds, then for each mode `steps` back-to-back calls
-    between HIP events on the current stream. Returns (wall_s, {mode: avg_s})."""
+    """Runs `warmup` untimed rounds, then times `steps` calls per mode between HIP
+    events on the current stream. With two modes the calls run as four back-to-back
+    batches in mirrored order - first half of mode A, first half of mode B, second
+    half of B, second half of A - so neither mode is always the one timed right after
+    the warmup. Returns (wall_s, {mode: avg_s})."""
     import torch
 
     q, k, v = inputs
     for _ in range(warmup):
         for causal in modes:
             entry(q, k, v, causal)
+    first = steps // 2
+    halves = [(causal, first) for causal in modes] + [(causal, steps - first) for causal in reversed(modes)]
+    halves = [(causal, n) for causal, n in halves if n > 0]
     stream = torch.cuda.current_stream()
-    events = [torch.cuda.Event(enable_timing=True) for _ in range(len(modes) + 1)]
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(len(halves) + 1)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     events[0].record(stream)
-    for i, causal in enumerate(modes):
-        for _ in range(steps):
+    for i, (causal, n) in enumerate(halves):
+        for _ in range(n):
             entry(q, k, v, causal)
         events[i + 1].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per_kernel = {("causal" if causal else "noncausal"): events[i].elapsed_time(events[i + 1]) / 1e3 / steps
-                  for i, causal in enumerate(modes)}
-    return wall, per_kernel
+    per_kernel = {}
+    for i, (causal, n) in enumerate(halves):
+        mode = "causal" if causal else "noncausal"
+        per_kernel[mode] = per_kernel.get(mode, 0.0) + events[i].elapsed_time(events[i + 1]) / 1e3
+    return wall, {mode: total / steps for mode, total in per_kernel.items()}
 
 
 def time_in_graph(entry, inputs, modes, steps, replays=3):
@@ -192,13 +201,49 @@ def run_single(entry, args):
     return 0
 
 
+def _cpu_rate(batch, heads, seq_len, causal, sigma, budget_s, chunk=None, max_heads=None):
+    """Times the oracle (FP32 torch on the CPU) on one workload: whole calls, or - for
+    configurations whose score tensor does not fit (chunk set) - one (batch, head) at a
+    time with the queries in chunks of `chunk` rows, over at most `max_heads` heads or
+    until `budget_s` is spent. Returns (algorithmic FLOP/s, description)."""
+    from oracle import attention_reference, attention_rows_fp32
+
+    q, k, v = make_inputs(batch, heads, seq_len, sigma=sigma)
+    if chunk is None:
+        attention_reference(q, k, v, causal=causal)  # warmup
+        runs, t0 = 0, time.perf_counter()
+        while runs < 3 or time.perf_counter() - t0 < budget_s:
+            attention_reference(q, k, v, causal=causal)
+            runs += 1
+        elapsed = time.perf_counter() - t0
+        flops = runs * attention_flops(batch, heads, seq_len, 64, causal)
+        return flops / elapsed, f"{runs} calls"
+    done, t0 = 0, time.perf_counter()
+    for bh in range(batch * heads):
+        b, h = divmod(bh, heads)
+        for i0 in range(0, seq_len, chunk):
+            rows = [(b, h, i) for i in range(i0, min(seq_len, i0 + chunk))]
+            attention_rows_fp32(q, k, v, rows, causal=causal)
+        done += 1
+        if (max_heads and done >= max_heads) or time.perf_counter() - t0 >= budget_s:
+            break
+    elapsed = time.perf_counter() - t0
+    flops = done * attention_flops(1, 1, seq_len, 64, causal)
+    return flops / elapsed, f"{done} of {batch * heads} heads, queries in chunks of {chunk}"
+
+
 def cpu_baseline(budget_s):
-    """Oracle (FP32 torch restatement of the reference) on this host's CPU cores."""
+    """Oracle (FP32 torch restatement of the reference) on this host's CPU cores, with
+    torch using os.cpu_count() threads. `value` is the headline workload (one
+    noncausal plus one causal B1 H8 N1024 call per step); `configs` holds the same
+    rate for the other BASELINE configurations on bounded samples. The CPU computes
+    every score even when causal; TFLOP/s use the algorithmic FLOPs (causal halved),
+    as the GPU figures do."""
     import torch
 
     from oracle import attention_reference
 
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     q, k, v = make_inputs(1, 8, 1024)
     flops = 0.0
@@ -211,11 +256,26 @@ def cpu_baseline(budget_s):
             flops += attention_flops(1, 8, 1024, 64, causal)
         runs += 1
     elapsed = time.perf_counter() - t0
+    configs = {}
+    for n in (128, 256, 512, 1024):
+        for causal in (False, True):
+            rate, how = _cpu_rate(1, 8, n, causal, 1.0, budget_s / 16)
+            configs[f"B1H8N{n}_{'causal' if causal else 'noncausal'}"] = {"tflops": round(rate / 1e12, 5),
+                                                                            "sample": how}
+    for causal in (False, True):
+        rate, how = _cpu_rate(16, 16, 4096, causal, 1.0, budget_s / 2, chunk=4096, max_heads=8)
+        configs[f"B16H16N4096_{'causal' if causal else 'noncausal'}"] = {"tflops": round(rate / 1e12, 5),
+                                                                           "sample": how}
+    rate, how = _cpu_rate(2, 32, 16384, True, 2.0, budget_s, chunk=2048, max_heads=2)
+    configs["B2H32N16384_causal_sigma2"] = {"tflops": round(rate / 1e12, 5), "sample": how}
     return {"value": round(flops / elapsed / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
             "kind": "port",
             "sample": f"{runs} steps of B1 H8 N1024 D64 (one noncausal + one causal "
-                      f"oracle.attention_reference call each, FP32 CPU), {elapsed:.1f} s",
-            "ms_per_step": round(elapsed / runs * 1e3, 3)}
+                      f"oracle.attention_reference call each, FP32 CPU), {elapsed:.1f} s; "
+                      f"configs: the other BASELINE configurations on the samples named",
+            "ms_per_step": round(elapsed / runs * 1e3, 3),
+            "affinity_cpus": len(os.sched_getaffinity(0)),
+            "configs": configs}
 
 
 def main() -> int:

@@ -879,7 +879,21 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_splitk_kernel(const _
 // LDS: four 16 KiB stages (K then V), tile t in stage t % 4, fetched three tiles
 // ahead by LDS-DMA (inline assembly: the compiler adds no waits for it; the loop
 // waits with explicit vmcnt) with one barrier per tile.
-template <bool kCausal>
+//
+// Causal schedules (kPairs):
+//  - false: one query tile per workgroup. Heads are taken kLptHeads at a time, and
+//    within such a group the query tiles run heaviest first across all its heads
+//    (every head's last tile, then every head's second-to-last, ...). The group's
+//    workgroups start on the same keys together, so its heads' K/V is read from
+//    HBM once and shared through L2, and the longest-first order drains the
+//    workgroup slots of the chip evenly.
+//  - true: a workgroup runs query tile T-1-p and then tile p of one head (T even),
+//    so every workgroup streams the same 4(T+1) key tiles: better when the grid is
+//    only one or two rounds of workgroups, where the group order has too few tiles
+//    to balance; the light pass re-reads keys that have left L2.
+constexpr uint32_t kLptHeads = 8;
+
+template <bool kCausal, bool kPairs>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
                                  const _Float16* __restrict__ key,
@@ -900,24 +914,36 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
     const int lq = lane & 31;
     const int half = lane >> 5;
 
-    // Workgroup -> (batch*head, work item), XCD-contiguous. Noncausal: an item is
-    // one query tile. Causal with an even number T of query tiles per head: an item
-    // is the pair of tiles T-1-p and p, heaviest first, so every workgroup streams
-    // the same 4(T+1) key tiles and the workgroup slots of the chip drain together
-    // (one tile per workgroup left the busiest CUs 25% above the mean). Causal with
-    // T odd: one tile per workgroup, heaviest first (pairing would leave the middle
-    // tile's workgroup with half the work).
+    // Workgroup -> (batch*head, work item), XCD-contiguous: dispatch is round-robin
+    // over the 8 XCDs (id % 8), so every XCD gets a contiguous range of logical items.
+    // Noncausal: an item is one query tile. Causal: see the schedules above; `item`
+    // counts from the heaviest tile (item 0 = tile T-1).
+    static_assert(kCausal || !kPairs, "pairs are a causal schedule");
     const uint32_t groups = gridDim.x;
     const uint32_t xcd = blockIdx.x & 7u;
     const uint32_t slot = blockIdx.x >> 3;
     const uint32_t per_xcd = groups >> 3;
     const uint32_t extra = groups & 7u;
     const uint32_t logical = xcd * per_xcd + min(xcd, extra) + slot;
-    const bool paired = kCausal && (num_query_tiles & 1) == 0;
-    const uint32_t items = paired ? (uint32_t)num_query_tiles / 2u : (uint32_t)num_query_tiles;
-    const uint32_t bh = logical / items;
-    const uint32_t item = logical - bh * items;
-    const int passes = paired ? 2 : 1;
+    const uint32_t tiles_per_head = (uint32_t)num_query_tiles;
+    const uint32_t batch_heads = kPairs ? groups * 2u / tiles_per_head : groups / tiles_per_head;
+    uint32_t bh, item;
+    if (kCausal && !kPairs && (batch_heads & 7u) == 0) {
+        // Every XCD owns batch_heads / 8 whole heads (slots 0.. of its dispatch order)
+        // and runs them kLptHeads at a time, heaviest tiles of the group first.
+        const uint32_t xcd_heads = batch_heads >> 3;
+        const uint32_t group = slot / (kLptHeads * tiles_per_head);
+        const uint32_t in_group = slot - group * (kLptHeads * tiles_per_head);
+        const uint32_t heads = min(kLptHeads, xcd_heads - group * kLptHeads);  // the last group may be short
+        item = in_group / heads;
+        bh = xcd * xcd_heads + group * kLptHeads + (in_group - item * heads);
+    } else {
+        // Head-major; a causal head's tiles heaviest first (or its pairs).
+        const uint32_t items = kPairs ? tiles_per_head / 2u : tiles_per_head;
+        bh = logical / items;
+        item = logical - bh * items;
+    }
+    constexpr int passes = kPairs ? 2 : 1;
 
     const size_t head_offset = (size_t)bh * (size_t)seq_len * kHeadDim;
     const _Float16* __restrict__ q_head = query + head_offset;
@@ -1193,16 +1219,28 @@ hipError_t launch_forward(const void* q, const void* k, const void* v, void* o,
     return hipGetLastError();
 }
 
-template <bool kCausal>
+template <bool kCausal, bool kPairs>
 hipError_t launch_wide(const void* q, const void* k, const void* v, void* o, int64_t batch_heads,
                        int64_t seq_len, float scale_log2, hipStream_t stream) {
     const int64_t query_tiles = seq_len / 256;
-    const int64_t items = kCausal && query_tiles % 2 == 0 ? query_tiles / 2 : query_tiles;  // causal: tile pairs
-    hipLaunchKernelGGL((fa2_forward_d64_wide_kernel<kCausal>), dim3((unsigned)(batch_heads * items)),
+    const int64_t items = kPairs ? query_tiles / 2 : query_tiles;
+    hipLaunchKernelGGL((fa2_forward_d64_wide_kernel<kCausal, kPairs>), dim3((unsigned)(batch_heads * items)),
                        dim3(256), 0, stream, static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
                        static_cast<const _Float16*>(v), static_cast<_Float16*>(o), (int)seq_len,
                        (int)query_tiles, scale_log2);
     return hipGetLastError();
+}
+
+// Causal 256-query problems run one query tile per workgroup in the head-group order
+// when every XCD owns whole heads (batch*heads a multiple of 8) and the grid has
+// enough tiles to balance; otherwise pairs of tiles (T even). Measured on MI355X
+// (same process, pairs -> head groups): -4% to -5% at 1024 tiles with T >= 8
+// (B8 H16 N2048, B4 H16 N4096, B1 H64 N4096), -2% to -4% at 2048 tiles (B32 H16 N1024,
+// B16 H16 N2048, B8 H16 N4096), -1% to -3% at 4096 (B16 H16 N4096, B2 H32 N16384);
+// +2% at B16 H16 N1024 (1024 tiles of T = 4).
+bool use_head_groups(int64_t batch_heads, int64_t tiles_per_head) {
+    if (batch_heads % 8 != 0) return false;
+    return tiles_per_head >= 8 || batch_heads * tiles_per_head >= 2048;
 }
 
 // 256-query workgroups (64 queries per wave) once the grid fills every workgroup
@@ -1239,8 +1277,11 @@ constexpr int64_t kEightWaveMinKeys = 2048;
 
 // The kernel a forward call with these sizes runs (the single place the choice is made).
 fa2_forward_kernel choose_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
-    if (use_wide_kernel(batch_heads, seq_len, causal))
-        return causal && (seq_len / 256) % 2 == 0 ? FA2_KERNEL_256_QUERY_PAIRS : FA2_KERNEL_256_QUERY;
+    if (use_wide_kernel(batch_heads, seq_len, causal)) {
+        const int64_t tiles = seq_len / 256;
+        return causal && tiles % 2 == 0 && !use_head_groups(batch_heads, tiles) ? FA2_KERNEL_256_QUERY_PAIRS
+                                                                               : FA2_KERNEL_256_QUERY;
+    }
     if (seq_len % kQueryTileAlign == 0 && use_128_query_kernel(batch_heads, seq_len, causal))
         return FA2_KERNEL_128_QUERY;
     const int64_t query_blocks = (seq_len + kQueriesPerWave - 1) / kQueriesPerWave;
@@ -1282,9 +1323,11 @@ int forward(const void* query, const void* key, const void* value, void* output,
     hipError_t err;
     switch (choose_kernel(batch_heads, seq_len, causal)) {
         case FA2_KERNEL_256_QUERY:
+            err = causal ? launch_wide<true, false>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
+                         : launch_wide<false, false>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
+            break;
         case FA2_KERNEL_256_QUERY_PAIRS:
-            err = causal ? launch_wide<true>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
-                         : launch_wide<false>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
+            err = launch_wide<true, true>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
             break;
         case FA2_KERNEL_128_QUERY:
             err = causal ? launch_forward<true, 4>(query, key, value, output, batch_heads, seq_len, scale_log2, s)

@@ -128,7 +128,8 @@ int main(void) {
     CHECK(fa2_forward_production_128x128(NULL, NULL, NULL, NULL, 0, H, N, D, 1, NULL) == FA2_STATUS_SUCCESS, "empty batch");
     CHECK(fa2_forward_tensorcore(q, k, v, o, B, H, N, D, 8, NULL) == FA2_STATUS_BAD_KEY_TILE, "key tile 8");
     CHECK(fa2_forward_plan(B, H, N, 0) == FA2_KERNEL_KEY_SPLIT_64, "plan %d", fa2_forward_plan(B, H, N, 0));
-    CHECK(fa2_forward_plan(16, 16, 4096, 1) == FA2_KERNEL_256_QUERY_PAIRS, "plan big causal");
+    CHECK(fa2_forward_plan(16, 16, 4096, 1) == FA2_KERNEL_256_QUERY, "plan big causal");
+    CHECK(fa2_forward_plan(16, 16, 1024, 1) == FA2_KERNEL_256_QUERY_PAIRS, "plan causal pairs");
     CHECK(strcmp(fa2_status_string(FA2_STATUS_BAD_HEAD_DIM), "head dimension must equal 64") == 0, "status text");
 
     hipFree(q);

@@ -172,7 +172,8 @@ int main(void) {
 
     CHECK(fa2_forward_plan(1, 8, 1024, 0) == FA2_KERNEL_KEY_SPLIT_64, "plan bench size");
     CHECK(fa2_forward_plan(16, 16, 4096, 0) == FA2_KERNEL_256_QUERY, "plan throughput size");
-    CHECK(fa2_forward_plan(16, 16, 4096, 1) == FA2_KERNEL_256_QUERY_PAIRS, "plan throughput size causal");
+    CHECK(fa2_forward_plan(16, 16, 4096, 1) == FA2_KERNEL_256_QUERY, "plan throughput size causal");
+    CHECK(fa2_forward_plan(16, 16, 1024, 1) == FA2_KERNEL_256_QUERY_PAIRS, "plan causal pairs");
 
     if (failures) {
         fprintf(stderr, "%d check(s) failed\n", failures);

@@ -54,10 +54,15 @@ K = capi
     (16, 16, 4096, False, K.FA2_KERNEL_256_QUERY), (1, 32, 1024, False, K.FA2_KERNEL_128_QUERY),
     (1, 31, 1024, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 8, 1024, False, K.FA2_KERNEL_KEY_SPLIT_64),
     (1, 9, 1024, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 8, 128, False, K.FA2_KERNEL_KEY_SPLIT_64),
-    # Causal: pairs of 256-query tiles from 512 workgroups when a head has an even
-    # number of tiles, single tiles from 2048 with an odd number.
-    (16, 16, 4096, True, K.FA2_KERNEL_256_QUERY_PAIRS), (1, 256, 1024, True, K.FA2_KERNEL_256_QUERY_PAIRS),
-    (1, 255, 1024, True, K.FA2_KERNEL_128_QUERY), (2, 32, 16384, True, K.FA2_KERNEL_256_QUERY_PAIRS),
+    # Causal: 256-query from 512 workgroups of tile pairs when a head has an even
+    # number T of tiles, single tiles from 2048 with an odd number. Single tiles in
+    # head groups (batch*heads a multiple of 8) from T >= 8 or 2048 tiles; pairs below
+    # that and when batch*heads is not a multiple of 8.
+    (16, 16, 4096, True, K.FA2_KERNEL_256_QUERY), (1, 256, 1024, True, K.FA2_KERNEL_256_QUERY_PAIRS),
+    (1, 255, 1024, True, K.FA2_KERNEL_128_QUERY), (2, 32, 16384, True, K.FA2_KERNEL_256_QUERY),
+    (32, 16, 1024, True, K.FA2_KERNEL_256_QUERY), (1, 504, 1024, True, K.FA2_KERNEL_256_QUERY_PAIRS),
+    (8, 16, 2048, True, K.FA2_KERNEL_256_QUERY), (1, 64, 4096, True, K.FA2_KERNEL_256_QUERY),
+    (1, 66, 4096, True, K.FA2_KERNEL_256_QUERY_PAIRS), (1, 510, 1024, True, K.FA2_KERNEL_256_QUERY_PAIRS),
     (1, 410, 1280, True, K.FA2_KERNEL_256_QUERY), (1, 409, 1280, True, K.FA2_KERNEL_128_QUERY),
     (1, 64, 1024, True, K.FA2_KERNEL_128_QUERY), (1, 63, 1024, True, K.FA2_KERNEL_KEY_SPLIT_32),
     (1, 8, 1024, True, K.FA2_KERNEL_KEY_SPLIT_64),

@@ -138,6 +138,35 @@ def test_throughput_shape_b16_h16_n4096(causal):
 
 
 @pytest.mark.parametrize("causal", [False, True])
+def test_whole_heads_b16_h16_n4096(causal):
+    # Every row of six whole heads of the throughput shape: the first and last, the two
+    # heads on each side of the first head-group boundary (8 heads per group) and of the
+    # first XCD range (heads 32x..32x+31 run on XCD x in both modes).
+    q, k, v = _inputs(16, 16, 4096, seed=61)
+    assert capi.forward_plan(16, 16, 4096, causal) == capi.FA2_KERNEL_256_QUERY
+    out = _run(q, k, v, causal).cpu()
+    assert torch.isfinite(out).all()
+    for bh in (0, 7, 8, 31, 32, 255):
+        b, h = divmod(bh, 16)
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        expected = attention_reference_fp32(q[sl], k[sl], v[sl], causal=causal)
+        _assert_close_to_oracle(out[sl], expected)
+
+
+def test_whole_head_b2_h32_n16384_sigma2_causal():
+    # One whole head (the last) of the long-context shape, every one of its 16384 rows,
+    # with the oracle evaluated in chunks of 2048 rows.
+    q, k, v = _inputs(2, 32, 16384, seed=0, sigma=2.0)
+    assert capi.forward_plan(2, 32, 16384, True) == capi.FA2_KERNEL_256_QUERY
+    out = _run(q, k, v, True).cpu()
+    b, h = 1, 31
+    for i0 in range(0, 16384, 2048):
+        rows = [(b, h, i) for i in range(i0, i0 + 2048)]
+        expected = attention_rows_fp32(q, k, v, rows, causal=True)
+        _assert_close_to_oracle(out[b, h, i0:i0 + 2048], expected)
+
+
+@pytest.mark.parametrize("causal", [False, True])
 def test_full_size_properties_b16_h16_n4096(causal):
     # Size-independent properties at the throughput shape, on the device, with no oracle:
     # * linearity in V - the probabilities depend on Q and K only, so the FP32 O of
@@ -225,12 +254,17 @@ def test_long_single_head_n2pow20(causal):
 
 
 @pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("shape", [(1, 64, 1024), (1, 8, 1024)])
+@pytest.mark.parametrize("shape", [(1, 64, 1024), (1, 8, 1024), (1, 9, 1024), (3, 3, 1024), (1, 4, 2048),
+                                   (1, 2, 4096)])
 def test_growing_scores_match_oracle(shape, causal):
     # Key norms ramp up 12x along the sequence, so the running max keeps growing (by
     # some 50 log2 units over a row) and the kernels' stale-max probabilities overflow
     # the 2^14 tile-sum bound several times per row: exercises the exact-max
-    # recompute path (both the 128-query and the key-split kernels).
+    # recompute path of the 128-query kernel and of every key-split variant (64-key
+    # tiles; 32-key tiles; 8 waves).
+    assert capi.forward_plan(*shape, causal) in (
+        capi.FA2_KERNEL_128_QUERY, capi.FA2_KERNEL_KEY_SPLIT_64, capi.FA2_KERNEL_KEY_SPLIT_32,
+        capi.FA2_KERNEL_KEY_SPLIT_8_WAVES)
     q, k, v = _inputs(*shape, seed=9)
     ramp = torch.linspace(1.0, 12.0, shape[2]).view(1, 1, -1, 1)
     k = (k.float() * ramp).half()
@@ -239,18 +273,37 @@ def test_growing_scores_match_oracle(shape, causal):
     _assert_close_to_oracle(out, attention_reference_fp32(q, k, v, causal=causal))
 
 
+@pytest.mark.parametrize("shape", [(1, 4, 2000), (1, 2, 2064)])
+def test_growing_scores_on_partial_key_tiles(shape):
+    # The partial-tile key-split instantiations (sequence lengths that are multiples of
+    # 16 only, through the Bc16 entry): 64-key tiles below 2048 keys, 8 waves with
+    # 32-key tiles from 2048 on, keys masked past the end. Ramped key norms force the
+    # exact-max recompute on the partial tiles too.
+    batch, heads, seq_len = shape
+    assert capi.forward_plan(batch, heads, seq_len, False) in (capi.FA2_KERNEL_KEY_SPLIT_64,
+                                                               capi.FA2_KERNEL_KEY_SPLIT_8_WAVES)
+    q, k, v = _inputs(batch, heads, seq_len, seed=19)
+    k = (k.float() * torch.linspace(1.0, 12.0, seq_len).view(1, 1, -1, 1)).half()
+    out = capi.forward_tensorcore(q.cuda(), k.cuda(), v.cuda(), key_tile=16)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    _assert_close_to_oracle(out, attention_reference_fp32(q, k, v, causal=False))
+
+
 @pytest.mark.parametrize("step", [13.5, 14.5])
 @pytest.mark.parametrize("causal, shape", [(False, (1, 8, 1024)), (True, (1, 8, 1024)),
                                            (False, (1, 64, 1024)), (True, (1, 64, 1024)),
-                                           (False, (8, 16, 1024)), (True, (8, 64, 1024))])
+                                           (False, (8, 16, 1024)), (True, (8, 64, 1024)),
+                                           (False, (1, 9, 1024)), (True, (3, 3, 1024)),
+                                           (False, (1, 4, 2048)), (True, (1, 2, 4096))])
 def test_scores_stepping_across_the_rescale_bound(causal, shape, step):
     # The kernels keep a stale running max until some probability would exceed 2^14
     # (2^14 + 2^14 is the largest pair their FP16 row sums add without overflow).
     # Keys 0..63 score 0 and every later key scores `step` log2 units higher, so after
     # the first key tile each probability is 2^13.5 (kept: the tile sums fail the
     # check but the exact max stays within the bound) or 2^14.5 (rescaled). A bound
-    # above 2^14 would overflow those pair sums to inf. Key-split, 128-query and
-    # 256-query kernels.
+    # above 2^14 would overflow those pair sums to inf. Key-split (64-key tiles,
+    # 32-key tiles, 8 waves), 128-query and 256-query kernels.
     batch, heads, seq_len = shape
     gen = torch.Generator().manual_seed(17)
     q = torch.ones(batch, heads, seq_len, 64).half()
@@ -265,17 +318,23 @@ def test_scores_stepping_across_the_rescale_bound(causal, shape, step):
 
 
 @pytest.mark.parametrize("ramp", [False, True])
-@pytest.mark.parametrize("causal, shape", [(False, (8, 16, 1024)), (True, (8, 64, 1024)),
-                                             (True, (2, 64, 2048)), (True, (4, 128, 1280)),
-                                             (True, (8, 64, 512))])
-def test_wide_workgroup_shapes_match_oracle(causal, shape, ramp):
+@pytest.mark.parametrize("causal, shape, kernel", [
+    (False, (8, 16, 1024), capi.FA2_KERNEL_256_QUERY),
+    (True, (8, 64, 1024), capi.FA2_KERNEL_256_QUERY), (True, (2, 64, 2048), capi.FA2_KERNEL_256_QUERY),
+    (True, (4, 128, 1280), capi.FA2_KERNEL_256_QUERY), (True, (1, 410, 1280), capi.FA2_KERNEL_256_QUERY),
+    (True, (8, 64, 512), capi.FA2_KERNEL_256_QUERY_PAIRS), (True, (1, 260, 1024), capi.FA2_KERNEL_256_QUERY_PAIRS),
+    (True, (1, 130, 2048), capi.FA2_KERNEL_256_QUERY_PAIRS)])
+def test_wide_workgroup_shapes_match_oracle(causal, shape, kernel, ramp):
     # Large enough for the 256-query kernel (64 queries per wave as two 32-query
     # blocks): every row of three whole heads - all four waves, both blocks of each
     # wave and, causal, every diagonal tile - plus sampled rows of the others. With
     # `ramp` the key norms grow 5x along the sequence, forcing the recompute path.
-    # Causal workgroups run query tiles T-1-p then p of a head with T even (T = 2, 4
-    # and 8 here, T = 8 at the smallest paired grid), one tile each with T odd (5).
+    # Causal schedules: one query tile per workgroup in groups of heads per XCD
+    # (batch*heads a multiple of 8: T = 4, 8 and 5 query tiles per head here), one tile
+    # per workgroup head by head (T = 5, batch*heads = 410), and pairs of tiles T-1-p, p
+    # (T = 2; T = 4 and 8 with batch*heads not a multiple of 8).
     batch, heads, seq_len = shape
+    assert capi.forward_plan(batch, heads, seq_len, causal) == kernel
     q, k, v = _inputs(*shape, seed=13)
     if ramp:
         k = (k.float() * torch.linspace(1.0, 5.0, seq_len).view(1, 1, -1, 1)).half()

@@ -1,8 +1,10 @@
 """GPU parity on both sides of every kernel-choice threshold of the forward.
 
 The forward picks its kernel from (batch*heads, seq_len, causal) (fa2_forward.hip,
-`forward`): the 256-query kernel from 512 workgroups (causal: pairs of query tiles
-when a head has an even number of them, else one tile per workgroup from 2048), the
+`choose_kernel`): the 256-query kernel from 512 workgroups (causal: one query tile per
+workgroup in per-XCD head groups when batch*heads is a multiple of 8 and a head has at
+least 8 tiles or the grid 2048; else pairs of query tiles when a head has an even
+number of them, one tile per workgroup from 2048 when odd), the
 128-query kernel from 256 (noncausal) or 512 (causal) groups of 128 queries, and
 otherwise the key-split kernel: up to 256 query blocks of 32, 4 waves with 64-key tiles
 (8 waves with 32-key tiles from 2048 keys on), and 32-key tiles beyond. Each case below sits one step below or at a threshold, and
@@ -47,6 +49,10 @@ CASES = [
     (1, 8, 2048, True, "key-split, 32-key tiles (512 query blocks of 2048 keys)", K.FA2_KERNEL_KEY_SPLIT_32),
     (2, 256, 256, False, "256-query (512 groups, the shortest key stream: 4 tiles)", K.FA2_KERNEL_256_QUERY),
     (8, 256, 256, True, "256-query, single tiles (2048 heads of one query tile)", K.FA2_KERNEL_256_QUERY),
+    (1, 504, 1024, True, "256-query, tile pairs (2016 tiles of T = 4)", K.FA2_KERNEL_256_QUERY_PAIRS),
+    (32, 16, 1024, True, "256-query, head groups (2048 tiles of T = 4)", K.FA2_KERNEL_256_QUERY),
+    (1, 64, 4096, True, "256-query, head groups (1024 tiles of T = 16)", K.FA2_KERNEL_256_QUERY),
+    (1, 66, 4096, True, "256-query, tile pairs (batch*heads not a multiple of 8)", K.FA2_KERNEL_256_QUERY_PAIRS),
 ]
 
 

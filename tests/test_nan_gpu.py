@@ -1,0 +1,98 @@
+"""NaN inputs on the GPU: which output rows the kernels make NaN, against the oracle.
+
+The reference's FP32 formula (flash_attention/reference.py:46-59) propagates a NaN in
+Q, K or V through the scores, the softmax and P.V. The kernels are compiled with
+-fno-honor-nans (their running max uses v_max_f32, which returns the non-NaN operand),
+and they follow the formula for every output row that sees the NaN:
+* a NaN in query row i makes row i NaN (every dimension) and leaves the others as the
+  oracle computes them;
+* a NaN in key row j makes every row that sees key j NaN (noncausal: all rows; causal:
+  rows i >= j); causal rows i < j are masked before the softmax in both and match;
+* a NaN in value (j, d) makes dimension d NaN in every row that sees key j, and no
+  other dimension.
+One case is not covered: causal rows i < j with a NaN in value row j. The formula's
+P.V multiplies their zero probability by the NaN (0 * NaN = NaN in every row of the
+head); the kernels skip key tiles past a row's diagonal, so such a row is NaN only when
+key j falls in a key tile its wave computes.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import flash_attention_2_lab_amd as fa
+from flash_attention_2_lab_amd import capi
+from oracle import attention_reference_fp32
+
+pytestmark = pytest.mark.gpu
+
+ENTRY = fa.flash_attention_cuda.tensorcore_attention_forward_production_128x128
+
+SHAPES = [
+    ((1, 8, 1024), False, capi.FA2_KERNEL_KEY_SPLIT_64), ((1, 8, 1024), True, capi.FA2_KERNEL_KEY_SPLIT_64),
+    ((1, 64, 1024), False, capi.FA2_KERNEL_128_QUERY), ((1, 64, 1024), True, capi.FA2_KERNEL_128_QUERY),
+    ((8, 16, 1024), False, capi.FA2_KERNEL_256_QUERY), ((8, 64, 1024), True, capi.FA2_KERNEL_256_QUERY),
+    ((8, 64, 512), True, capi.FA2_KERNEL_256_QUERY_PAIRS), ((1, 4, 2048), False, capi.FA2_KERNEL_KEY_SPLIT_8_WAVES),
+]
+IDS = [f"{'causal' if c else 'noncausal'}-{b}x{h}x{n}" for (b, h, n), c, _ in SHAPES]
+
+
+def _inputs(shape, seed):
+    gen = torch.Generator().manual_seed(seed)
+    return tuple(torch.randn((*shape, 64), generator=gen).half() for _ in range(3))
+
+
+def _check(out, expected, nan_mask):
+    """NaN exactly where nan_mask is set; elsewhere within the north-star gate."""
+    out = out.float().cpu()
+    assert torch.equal(torch.isnan(out), nan_mask)
+    keep = ~nan_mask
+    torch.testing.assert_close(out[keep], expected[keep], atol=2e-3, rtol=1e-2)
+
+
+@pytest.mark.parametrize("shape, causal, kernel", SHAPES, ids=IDS)
+def test_nan_in_query_row(shape, causal, kernel):
+    assert capi.forward_plan(*shape, causal) == kernel
+    q, k, v = _inputs(shape, seed=71)
+    n = shape[2]
+    b, h, i = shape[0] - 1, shape[1] // 2, n // 2 + 5
+    q[b, h, i, 17] = float("nan")
+    expected = attention_reference_fp32(q, k, v, causal=causal)
+    mask = torch.zeros(expected.shape, dtype=torch.bool)
+    mask[b, h, i] = True
+    assert torch.equal(torch.isnan(expected), mask)
+    _check(ENTRY(q.cuda(), k.cuda(), v.cuda(), causal), expected, mask)
+
+
+@pytest.mark.parametrize("shape, causal, kernel", SHAPES, ids=IDS)
+def test_nan_in_key_row(shape, causal, kernel):
+    assert capi.forward_plan(*shape, causal) == kernel
+    q, k, v = _inputs(shape, seed=72)
+    n = shape[2]
+    b, h, j = 0, shape[1] - 1, n // 3
+    k[b, h, j, 40] = float("nan")
+    expected = attention_reference_fp32(q, k, v, causal=causal)
+    mask = torch.zeros(expected.shape, dtype=torch.bool)
+    mask[b, h, j if causal else 0:] = True
+    assert torch.equal(torch.isnan(expected), mask)
+    _check(ENTRY(q.cuda(), k.cuda(), v.cuda(), causal), expected, mask)
+
+
+@pytest.mark.parametrize("shape, causal, kernel", SHAPES, ids=IDS)
+def test_nan_in_value_element(shape, causal, kernel):
+    assert capi.forward_plan(*shape, causal) == kernel
+    q, k, v = _inputs(shape, seed=73)
+    n = shape[2]
+    b, h, j, d = 0, 0, n - 70, 9
+    v[b, h, j, d] = float("nan")
+    expected = attention_reference_fp32(q, k, v, causal=causal)
+    out = ENTRY(q.cuda(), k.cuda(), v.cuda(), causal).float().cpu()
+    if causal:
+        # Rows before the key: compared outside dimension d only (see the module docstring).
+        out[b, h, :j, d] = 0.0
+        expected[b, h, :j, d] = 0.0
+    mask = torch.zeros(expected.shape, dtype=torch.bool)
+    mask[b, h, j if causal else 0:, d] = True
+    assert torch.equal(torch.isnan(expected), mask)
+    _check(out, expected, mask)

@@ -159,6 +159,18 @@ WORKLOADS = {
 }
 
 
+# North-star workloads timed after the headline: (workload key, modes).
+NORTH_STAR = (("b16h16n4096", (False, True)), ("b2h32n16384", (True,)))
+
+
+def traffic_keys():
+    """The rocprof traffic entries the bench line's roofline objects read."""
+    keys = [f"b1h8n1024/{m}" for m in ("noncausal", "causal")]
+    for workload, ns_modes in NORTH_STAR:
+        keys += [f"{workload}/{'causal' if c else 'noncausal'}" for c in ns_modes]
+    return keys
+
+
 # Plain device-to-device copy of a known size: calibrates the FETCH_SIZE and
 # WRITE_SIZE counters (each should read this many bytes per dispatch).
 COPY_CALIBRATION_BYTES = 256 << 20
@@ -346,21 +358,28 @@ def main() -> int:
     del inputs
 
     if not args.skip_north_star:
+        # Each north-star workload: 3 untimed calls per mode, then five timed batches of
+        # --north-star-steps calls (mirrored halves per mode, as above); the median batch
+        # gives `us`, and `us_batches` lists all five.
         north = {}
-        big = make_inputs(16, 16, 4096, device="cuda")
-        _, t = time_kernel_batches(entry, big, modes, args.north_star_steps, 3)
-        for mode, avg in t.items():
-            f = attention_flops(16, 16, 4096, 64, mode == "causal")
-            north[f"B16H16N4096_{mode}"] = {"us": round(avg * 1e6, 2), "tflops": round(f / avg / 1e12, 2),
-                                            "roofline": roofline(f, avg, f"b16h16n4096/{mode}")}
-        del big
-        long_ctx = make_inputs(2, 32, 16384, sigma=2.0, device="cuda")
-        _, t = time_kernel_batches(entry, long_ctx, (True,), max(3, args.north_star_steps // 4), 1)
-        f = attention_flops(2, 32, 16384, 64, True)
-        north["B2H32N16384_causal_sigma2"] = {"us": round(t["causal"] * 1e6, 2),
-                                              "tflops": round(f / t["causal"] / 1e12, 2),
-                                              "roofline": roofline(f, t["causal"], "b2h32n16384/causal")}
-        del long_ctx
+        for workload, ns_modes in NORTH_STAR:
+            batch, heads, seq_len, sigma = WORKLOADS[workload]
+            steps = args.north_star_steps if len(ns_modes) > 1 else max(2, args.north_star_steps // 4)
+            name = workload.upper()
+            data = make_inputs(batch, heads, seq_len, sigma=sigma, device="cuda")
+            batches = []
+            for rep in range(5):
+                _, t = time_kernel_batches(entry, data, ns_modes, steps, 3 if rep == 0 else 0)
+                batches.append(t)
+            del data
+            for mode in t:
+                per_call = sorted(b[mode] for b in batches)
+                avg = per_call[len(per_call) // 2]
+                f = attention_flops(batch, heads, seq_len, 64, mode == "causal")
+                key = f"{name}_{mode}" + ("_sigma2" if sigma != 1.0 else "")
+                north[key] = {"us": round(avg * 1e6, 2), "tflops": round(f / avg / 1e12, 2),
+                              "us_batches": [round(b[mode] * 1e6, 1) for b in batches],
+                              "roofline": roofline(f, avg, f"{workload}/{mode}")}
         line["north_star"] = north
 
     if not args.skip_cpu:

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define FA2_MI355X_ABI_VERSION 4
+#define FA2_MI355X_ABI_VERSION 5
 
 enum fa2_status {
     FA2_STATUS_SUCCESS = 0,
@@ -132,7 +132,9 @@ enum fa2_forward_kernel {
     FA2_KERNEL_KEY_SPLIT_64 = 4,     /* 32 queries per workgroup, keys split over 4 waves, */
                                      /* 64-key tiles                                       */
     FA2_KERNEL_KEY_SPLIT_32 = 5,     /* the same with 32-key tiles                         */
-    FA2_KERNEL_KEY_SPLIT_8_WAVES = 6 /* keys split over 8 waves, 32-key tiles              */
+    FA2_KERNEL_KEY_SPLIT_8_WAVES = 6, /* keys split over 8 waves, 32-key tiles             */
+    FA2_KERNEL_KEY_SPLIT_PAIRS16 = 7  /* causal: 16-query blocks p and N/16-1-p of a head  */
+                                      /* per workgroup, keys split over 4 waves            */
 };
 
 /*

@@ -122,7 +122,7 @@ int main(void) {
                 for (int causal = 0; causal <= 1; ++causal) {
                     const int64_t batch = counts[a], heads = counts[b], n = sizes[c];
                     const int plan = fa2_forward_plan(batch, heads, n, causal);
-                    CHECK(plan >= FA2_KERNEL_NONE && plan <= FA2_KERNEL_KEY_SPLIT_8_WAVES, "plan %d", plan);
+                    CHECK(plan >= FA2_KERNEL_NONE && plan <= FA2_KERNEL_KEY_SPLIT_PAIRS16, "plan %d", plan);
                     int none = batch <= 0 || heads <= 0 || n <= 0 || n > ((int64_t)1 << 24);
                     if (!none) none = batch > (int64_t)UINT32_MAX / heads;
                     if (!none) none = batch * heads > (int64_t)UINT32_MAX / ((n + 31) / 32);

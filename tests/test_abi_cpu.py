@@ -39,7 +39,7 @@ def test_status_codes_match_header():
 def test_kernel_ids_match_header():
     text = capi.HEADER_PATH.read_text()
     for name in ("NONE", "256_QUERY", "256_QUERY_PAIRS", "128_QUERY", "KEY_SPLIT_64", "KEY_SPLIT_32",
-                 "KEY_SPLIT_8_WAVES"):
+                 "KEY_SPLIT_8_WAVES", "KEY_SPLIT_PAIRS16"):
         value = int(re.search(rf"FA2_KERNEL_{name} = (\d+)", text).group(1))
         assert getattr(capi, f"FA2_KERNEL_{name}") == value
 
@@ -65,7 +65,9 @@ K = capi
     (1, 66, 4096, True, K.FA2_KERNEL_256_QUERY_PAIRS), (1, 510, 1024, True, K.FA2_KERNEL_256_QUERY_PAIRS),
     (1, 410, 1280, True, K.FA2_KERNEL_256_QUERY), (1, 409, 1280, True, K.FA2_KERNEL_128_QUERY),
     (1, 64, 1024, True, K.FA2_KERNEL_128_QUERY), (1, 63, 1024, True, K.FA2_KERNEL_KEY_SPLIT_32),
-    (1, 8, 1024, True, K.FA2_KERNEL_KEY_SPLIT_64),
+    (1, 8, 1024, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16), (1, 2, 128, True, K.FA2_KERNEL_KEY_SPLIT_64),
+    (1, 8, 896, True, K.FA2_KERNEL_KEY_SPLIT_64), (1, 2, 1024, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16),
+    (1, 4, 1920, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16), (1, 4, 1040, True, K.FA2_KERNEL_KEY_SPLIT_64),
     # Key-split shapes from 2048 keys on split each block's keys over 8 waves.
     (1, 2, 4096, False, K.FA2_KERNEL_KEY_SPLIT_8_WAVES), (1, 1, 2048, True, K.FA2_KERNEL_KEY_SPLIT_8_WAVES),
     (1, 4, 2048, False, K.FA2_KERNEL_KEY_SPLIT_8_WAVES), (1, 1, 8192, True, K.FA2_KERNEL_KEY_SPLIT_8_WAVES),

@@ -261,10 +261,10 @@ def test_growing_scores_match_oracle(shape, causal):
     # some 50 log2 units over a row) and the kernels' stale-max probabilities overflow
     # the 2^14 tile-sum bound several times per row: exercises the exact-max
     # recompute path of the 128-query kernel and of every key-split variant (64-key
-    # tiles; 32-key tiles; 8 waves).
+    # tiles; 32-key tiles; 8 waves; causal pairs of 16-query blocks).
     assert capi.forward_plan(*shape, causal) in (
         capi.FA2_KERNEL_128_QUERY, capi.FA2_KERNEL_KEY_SPLIT_64, capi.FA2_KERNEL_KEY_SPLIT_32,
-        capi.FA2_KERNEL_KEY_SPLIT_8_WAVES)
+        capi.FA2_KERNEL_KEY_SPLIT_8_WAVES, capi.FA2_KERNEL_KEY_SPLIT_PAIRS16)
     q, k, v = _inputs(*shape, seed=9)
     ramp = torch.linspace(1.0, 12.0, shape[2]).view(1, 1, -1, 1)
     k = (k.float() * ramp).half()

@@ -7,7 +7,8 @@ least 8 tiles or the grid 2048; else pairs of query tiles when a head has an eve
 number of them, one tile per workgroup from 2048 when odd), the
 128-query kernel from 256 (noncausal) or 512 (causal) groups of 128 queries, and
 otherwise the key-split kernel: up to 256 query blocks of 32, 4 waves with 64-key tiles
-(8 waves with 32-key tiles from 2048 keys on), and 32-key tiles beyond. Each case below sits one step below or at a threshold, and
+(8 waves with 32-key tiles from 2048 keys on; causal from 1024 to 2047 keys, pairs of
+16-query blocks), and 32-key tiles beyond. Each case below sits one step below or at a threshold, and
 `fa2_forward_plan` (the function the forward dispatches through) must name the kernel
 the case is meant to reach; every row of the first and last head and sampled rows of
 the others are checked against the FP32 oracle (atol 2e-3 + rtol 1e-2).
@@ -41,7 +42,11 @@ CASES = [
     (1, 410, 1280, True, "256-query, single tiles (2050, odd count per head)", K.FA2_KERNEL_256_QUERY),
     (1, 63, 1024, True, "key-split, 32-key tiles (504 groups of 128)", K.FA2_KERNEL_KEY_SPLIT_32),
     (1, 64, 1024, True, "128-query (512 groups of 128)", K.FA2_KERNEL_128_QUERY),
-    (1, 8, 1024, True, "key-split, 64-key tiles (256 query blocks)", K.FA2_KERNEL_KEY_SPLIT_64),
+    (1, 8, 1024, True, "key-split, pairs of 16-query blocks (256 pairs)", K.FA2_KERNEL_KEY_SPLIT_PAIRS16),
+    (1, 4, 1920, True, "key-split, pairs of 16-query blocks (the longest below 2048 keys)",
+     K.FA2_KERNEL_KEY_SPLIT_PAIRS16),
+    (1, 8, 896, True, "key-split, 64-key tiles (224 blocks below 1024 keys)", K.FA2_KERNEL_KEY_SPLIT_64),
+    (1, 2, 1024, True, "key-split, pairs of 16-query blocks (64 pairs)", K.FA2_KERNEL_KEY_SPLIT_PAIRS16),
     (3, 3, 1024, True, "key-split, 32-key tiles (288 query blocks)", K.FA2_KERNEL_KEY_SPLIT_32),
     (1, 4, 1024, False, "key-split, 64-key tiles (1024 keys)", K.FA2_KERNEL_KEY_SPLIT_64),
     (1, 4, 2048, False, "key-split, 8 waves (2048 keys, 256 query blocks)", K.FA2_KERNEL_KEY_SPLIT_8_WAVES),

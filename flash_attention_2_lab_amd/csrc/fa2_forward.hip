@@ -69,6 +69,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 #define FA2_LDS __attribute__((address_space(3)))
 
@@ -1230,11 +1231,13 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
     }
     constexpr int passes = kPairs ? 2 : 1;
 
+    // Q and O of the head through buffer descriptors (SGPR base, 32-bit lane offsets):
+    // no 64-bit row addresses stay live in VGPRs across the passes.
     const size_t head_offset = (size_t)bh * (size_t)seq_len * kHeadDim;
-    const _Float16* __restrict__ q_head = query + head_offset;
+    const __amdgpu_buffer_rsrc_t q_head = head_resource(query + head_offset, seq_len);
     const u32x4 k_head = head_descriptor(key + head_offset, seq_len);
     const u32x4 v_head = head_descriptor(value + head_offset, seq_len);
-    _Float16* __restrict__ o_head = output + head_offset;
+    const __amdgpu_buffer_rsrc_t o_head = head_resource(output + head_offset, seq_len);
 
     const uint32_t smem_addr = lds_address(smem);
     const int dma_off[2] = {dma_lane_offset(lane, 0), dma_lane_offset(lane, 1)};
@@ -1321,17 +1324,19 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
     // 32*dblk + 8*(i/4) + 4*half + i%4 of the lane's query.
     auto store = [&](const f32x16 (&o)[2], float l_run, int q) {
         const float inv_l = 1.0f / sum_across_halves(l_run);
-        _Float16* o_row = o_head + (size_t)q * kHeadDim;
+        const int row = q * kRowBytes + 8 * half;
 #pragma unroll
         for (int dblk = 0; dblk < 2; ++dblk)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const f16x2 a = pack_rn(o[dblk][4 * g + 0] * inv_l, o[dblk][4 * g + 1] * inv_l);
                 const f16x2 c = pack_rn(o[dblk][4 * g + 2] * inv_l, o[dblk][4 * g + 3] * inv_l);
-                *reinterpret_cast<f16x4*>(o_row + 32 * dblk + 8 * g + 4 * half) = __builtin_shufflevector(a, c, 0, 1, 2, 3);
+                const f16x4 v = __builtin_shufflevector(a, c, 0, 1, 2, 3);
+                __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), o_head, row + 64 * dblk + 16 * g, 0, 0);
             }
     };
 
+#pragma unroll
     for (int pass = 0; pass < passes; ++pass) {
         const uint32_t qtile = !kCausal ? item : pass == 0 ? (uint32_t)num_query_tiles - 1u - item : item;
         const int q_block = (int)qtile * kBlockM;
@@ -1348,8 +1353,8 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
         f16x8 qa[4], qb[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            qa[ks] = *reinterpret_cast<const f16x8*>(q_head + (size_t)query_a * kHeadDim + ks * 16 + half * 8);
-            qb[ks] = *reinterpret_cast<const f16x8*>(q_head + (size_t)query_b * kHeadDim + ks * 16 + half * 8);
+            qa[ks] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(q_head, query_a * kRowBytes + 32 * ks + 16 * half, 0, 0));
+            qb[ks] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(q_head, query_b * kRowBytes + 32 * ks + 16 * half, 0, 0));
         }
         dma_tile(0);
         dma_tile(1);  // num_tiles >= 4: seq_len and the causal key range are multiples of 256
@@ -1415,13 +1420,29 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
                 // Causal mask on the wave's diagonal tile (keys 64t.. = q_wave..): register
                 // i of block b holds key 64t + 32b + 16(i/8) + 8*half + i%8.
                 if (kCausal && t == wave_last_tile) {
+                    // Key offsets in the tile past which block a's query is masked (block
+                    // b's is 32 more). The sign of limit - offset selects -inf by bit
+                    // select: compares would be hoisted out of the loop as 64 lane masks
+                    // in SGPRs, and spill.
+                    // Per 8-key group one opaque base, so that every other constant is an
+                    // inline operand (0..7) rather than an SGPR.
+                    const int limit = query_a - t * kKeysPerTile - 8 * half;
+                    constexpr uint32_t kNegInf = 0xff800000u;
 #pragma unroll
                     for (int b = 0; b < 2; ++b)
 #pragma unroll
-                        for (int i = 0; i < 16; ++i) {
-                            const int key_index = t * kKeysPerTile + 32 * b + 16 * (i >> 3) + 8 * half + (i & 7);
-                            if (key_index > query_a) sa[b][i] = -INFINITY;
-                            if (key_index > query_b) sb[b][i] = -INFINITY;
+                        for (int hi = 0; hi < 2; ++hi) {
+                            int base_a = limit - (32 * b + 16 * hi);
+                            int base_b = base_a + 32;
+                            asm volatile("" : "+v"(base_a), "+v"(base_b));
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) {
+                                const int i = 8 * hi + j;  // key offset 32b + 16hi + 8half + j
+                                const uint32_t mask_a = (uint32_t)((base_a - j) >> 31);
+                                const uint32_t mask_b = (uint32_t)((base_b - j) >> 31);
+                                sa[b][i] = __uint_as_float((mask_a & kNegInf) | (~mask_a & __float_as_uint(sa[b][i])));
+                                sb[b][i] = __uint_as_float((mask_b & kNegInf) | (~mask_b & __float_as_uint(sb[b][i])));
+                            }
                         }
                 }
 

@@ -1167,17 +1167,25 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_pairs16_kernel(const 
 // waits with explicit vmcnt) with one barrier per tile.
 //
 // Causal schedules (kPairs):
-//  - false: one query tile per workgroup. Heads are taken kLptHeads at a time, and
-//    within such a group the query tiles run heaviest first across all its heads
-//    (every head's last tile, then every head's second-to-last, ...). The group's
-//    workgroups start on the same keys together, so its heads' K/V is read from
-//    HBM once and shared through L2, and the longest-first order drains the
-//    workgroup slots of the chip evenly.
+//  - false: one query tile per workgroup. Each XCD takes its own heads a group at a
+//    time, and within a group the query tiles run heaviest first across all its
+//    heads (every head's last tile, then every head's second-to-last, ...). A group
+//    has about as many tiles as an XCD has workgroup slots (64: 32 CUs, two
+//    workgroups each), so its workgroups start on the same keys together and its
+//    heads' K/V is read from HBM about once and shared through L2; the
+//    longest-first order drains the workgroup slots of the chip evenly.
 //  - true: a workgroup runs query tile T-1-p and then tile p of one head (T even),
 //    so every workgroup streams the same 4(T+1) key tiles: better when the grid is
 //    only one or two rounds of workgroups, where the group order has too few tiles
 //    to balance; the light pass re-reads keys that have left L2.
-constexpr uint32_t kLptHeads = 8;
+// Heads per group for T query tiles per head: 64 / T, from 1 to 8. Measured on
+// MI355X (same process): at T = 16 (B16 H16 N4096) groups of 4 run 2.6% faster than
+// groups of 8 and fetch 1.04x Q+K+V from HBM against 1.69x; at T = 64 (B2 H32 N16384)
+// one head per group fetches 1.13x against 6.9x for 8, within 1.3% of the fastest
+// group size.
+__device__ __forceinline__ uint32_t group_heads(uint32_t tiles_per_head) {
+    return tiles_per_head >= 64 ? 1u : tiles_per_head >= 32 ? 2u : tiles_per_head >= 16 ? 4u : 8u;
+}
 
 template <bool kCausal, bool kPairs>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
@@ -1216,13 +1224,14 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
     uint32_t bh, item;
     if (kCausal && !kPairs && (batch_heads & 7u) == 0) {
         // Every XCD owns batch_heads / 8 whole heads (slots 0.. of its dispatch order)
-        // and runs them kLptHeads at a time, heaviest tiles of the group first.
+        // and runs them a group at a time, heaviest tiles of the group first.
         const uint32_t xcd_heads = batch_heads >> 3;
-        const uint32_t group = slot / (kLptHeads * tiles_per_head);
-        const uint32_t in_group = slot - group * (kLptHeads * tiles_per_head);
-        const uint32_t heads = min(kLptHeads, xcd_heads - group * kLptHeads);  // the last group may be short
+        const uint32_t per_group = group_heads(tiles_per_head);
+        const uint32_t group = slot / (per_group * tiles_per_head);
+        const uint32_t in_group = slot - group * (per_group * tiles_per_head);
+        const uint32_t heads = min(per_group, xcd_heads - group * per_group);  // the last group may be short
         item = in_group / heads;
-        bh = xcd * xcd_heads + group * kLptHeads + (in_group - item * heads);
+        bh = xcd * xcd_heads + group * per_group + (in_group - item * heads);
     } else {
         // Head-major; a causal head's tiles heaviest first (or its pairs).
         const uint32_t items = kPairs ? tiles_per_head / 2u : tiles_per_head;

@@ -869,6 +869,12 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_splitk_kernel(const _
     }
 }
 
+// Key order of a 16-key MFMA block in the paired 16-query kernel: group g of 4 rows
+// holds keys 4 tau(g) + 0..3, tau = 0, 3, 1, 2 (table in a 16-bit word, 4 bits per entry).
+__device__ __forceinline__ int perm16_group(int g) { return (0x2130 >> (4 * g)) & 3; }
+__device__ __forceinline__ int perm16(int m) { return 4 * perm16_group(m >> 2) + (m & 3); }
+__device__ __forceinline__ int perm16_inverse(int row) { return 4 * ((0x1320 >> (4 * (row >> 2))) & 3) + (row & 3); }
+
 // Max and sum over lanes l, l^16, l^32, l^48: the four lanes that hold one query's
 // scores in the 16x16 MFMA layout.
 __device__ __forceinline__ float max_across_groups16(float x) {
@@ -890,7 +896,8 @@ __device__ __forceinline__ float max_across_groups16(float x) {
 // stages of its own, keeps a running max, sum and O per block, and the partial
 // results of each block are merged through LDS at the end. Scores come from
 // v_mfma_f32_16x16x32_f16 (S^T = K Q^T, 16 keys x 16 queries per MFMA): lane l holds
-// query l%16 and keys 16h + 4(l/16) + 0..3 of each 16-key block h, so the probabilities
+// query l%16 and four consecutive keys of each 16-key block h (the group l/16 with its
+// two bits swapped, times 4, + 0..3: K rows feed the MFMA in that order), so the probabilities
 // of a 32-key block are the lane's P^T operand of O^T += V^T P^T as they stand, with
 // V^T read by LDS transpose reads.
 template <int kSplit>
@@ -948,13 +955,18 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_pairs16_kernel(const 
     const uint32_t my_q_addr = my_stages_addr + 2 * kStageBytes;
     const int dma_off[2] = {dma_lane_offset(lane, 0), dma_lane_offset(lane, 1)};
 
-    // Both blocks' Q rows to this wave's LDS area, ahead of its first key tile.
+    // Both blocks' Q rows to this wave's LDS area, ahead of its first key tile, in the
+    // order the K rows feed the MFMA (LDS row perm16(j) holds query row j; see below):
+    // lane i of the DMA writes LDS row R = 8n + i/8 and so reads query row
+    // perm16_inverse(R).
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
-        for (int n = 0; n < kQBlockBytes / 1024; ++n)
-            dma16_asm(q_desc, my_q_addr + (uint32_t)(b * kQBlockBytes + n * 1024), dma_off[n & 1],
-                      (q0[b] + 8 * n) * kRowBytes);
+        for (int n = 0; n < kQBlockBytes / 1024; ++n) {
+            const int lds_row = 8 * n + (lane >> 3);
+            const int q_lane_off = perm16_inverse(lds_row) * kRowBytes + (((lane & 7) ^ tile_swizzle(lds_row)) << 4);
+            dma16_asm(q_desc, my_q_addr + (uint32_t)(b * kQBlockBytes + n * 1024), q_lane_off, q0[b] * kRowBytes);
+        }
     // Item j of the workgroup's list: key tile j of block 0, then key tile j - tiles0 of block 1.
     auto dma_item = [&](int j, int st) {
         const int t = j < tiles0 ? j : j - tiles0;
@@ -969,16 +981,26 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_pairs16_kernel(const 
     };
     if (t_begin < t_end) dma_item(t_begin, 0);
 
-    // Per-lane LDS offsets. K and Q (A and B operands of S^T = K Q^T): row lq of a
-    // 16-row block, dims 32ks + 8grp..+7 (chunk 4ks + grp).
-    const int swz_q = tile_swizzle(lq);
-    int kq_off[2];
+    // Per-lane LDS offsets. K (A operand of S^T = K Q^T): MFMA row lq of a 16-key block
+    // reads key row perm16(lq), dims 32ks + 8grp..+7 (chunk 4ks + grp). perm16 moves
+    // whole groups of 4 rows (group g to group tau(g), tau = 0, 3, 1, 2), so lane group
+    // grp holds the 4 consecutive keys 4 tau(grp) + 0..3 of each 16 and the V transpose
+    // reads stay 4-row reads; the order makes the 8 rows of every K read pass differ
+    // in bit 3 and the 8 rows of every V transpose pass differ in bit 2, which the
+    // swizzle maps to distinct banks (measured: 10k bank conflicts per launch at
+    // B1 H8 N1024 causal against 149k in natural order). Q (B operand): query lq, stored
+    // at LDS row perm16(lq) by the DMA above, so its reads spread the same way.
+    const int key_grp = perm16_group(grp);
+    const int k_row = perm16(lq);
+    const int swz_k = tile_swizzle(k_row);
+    int k_off[2];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) kq_off[ks] = lq * kRowBytes + (((4 * ks + grp) ^ swz_q) << 4);
+    for (int ks = 0; ks < 2; ++ks) k_off[ks] = k_row * kRowBytes + (((4 * ks + grp) ^ swz_k) << 4);
+    const int (&q_off)[2] = k_off;
     // V^T (A operand of O^T += V^T P^T) by transpose reads: in lane group grp, lane lq
-    // reads row 4grp + lq/4 (plus 16h + 32kb) at dims 16dblk + 4(lq%4)..+3; the read
+    // reads row 4key_grp + lq/4 (plus 16h + 32kb) at dims 16dblk + 4(lq%4)..+3; the read
     // returns to it dim 16dblk + lq at the group's four keys.
-    const int v_row = 4 * grp + (lq >> 2);
+    const int v_row = 4 * key_grp + (lq >> 2);
     const int swz_v = tile_swizzle(v_row);
     int v_off[4];
 #pragma unroll
@@ -994,7 +1016,7 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_pairs16_kernel(const 
         for (int d = 0; d < 4; ++d) o[b][d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     // Items [t_begin, t_end) in order; block 0's, then block 1's. Scores S[kb][h]:
-    // keys 32kb + 16h + 4grp + 0..3 of the tile, query q0 + lq.
+    // keys 32kb + 16h + 4key_grp + 0..3 of the tile, query q0 + lq.
     auto run_block = [&](auto block_tag, int j_begin, int j_end) {
         constexpr int b = decltype(block_tag)::value;
         f16x8 qf[2];
@@ -1009,7 +1031,7 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_pairs16_kernel(const 
             if (j == j_begin) {
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks)
-                    qf[ks] = *reinterpret_cast<const f16x8*>(my_q + b * kQBlockBytes + kq_off[ks]);
+                    qf[ks] = *reinterpret_cast<const f16x8*>(my_q + b * kQBlockBytes + q_off[ks]);
             }
             const uint8_t* k_lds = my_stages + st * kStageBytes;
             const uint8_t* v_lds = k_lds + kTileBytes;
@@ -1022,8 +1044,8 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_pairs16_kernel(const 
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const uint8_t* rows = k_lds + (32 * kb + 16 * h) * kRowBytes;
-                    const f16x8 k0 = *reinterpret_cast<const f16x8*>(rows + kq_off[0]);
-                    const f16x8 k1 = *reinterpret_cast<const f16x8*>(rows + kq_off[1]);
+                    const f16x8 k0 = *reinterpret_cast<const f16x8*>(rows + k_off[0]);
+                    const f16x8 k1 = *reinterpret_cast<const f16x8*>(rows + k_off[1]);
                     s[kb][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, qf[0], zero, 0, 0, 0);
                     s[kb][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qf[1], s[kb][h], 0, 0, 0);
                 }
@@ -1036,7 +1058,7 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_pairs16_kernel(const 
                     for (int h = 0; h < 2; ++h)
 #pragma unroll
                         for (int r = 0; r < 4; ++r)
-                            if (t * kKeysPerTile + 32 * kb + 16 * h + 4 * grp + r > my_query) s[kb][h][r] = -INFINITY;
+                            if (t * kKeysPerTile + 32 * kb + 16 * h + 4 * key_grp + r > my_query) s[kb][h][r] = -INFINITY;
             }
 
             // Online softmax with the lazy rescale (bound 2^kRescaleLog2): the first tile of

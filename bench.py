@@ -197,10 +197,49 @@ def run_copy_calibration(args):
     return 0
 
 
+# The vendor GEMM at the FP16 rate the attention kernels are priced against: one
+# 8192^3 product (the vendor BLAS through torch.matmul, FP32 accumulation), on N(0,1) and on
+# all-zero operands. It shows what the MFMA pipes sustain on random data at the board's
+# power limit, with no softmax.
+GEMM_SIZE = 8192
+
+
+def run_gemm_ceiling(args):
+    import torch
+
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    out = {"workload": "gemm", "m_n_k": GEMM_SIZE, "dtype": "fp16", "steps": args.steps}
+    for name in ("randn", "zeros"):
+        a = torch.randn(GEMM_SIZE, GEMM_SIZE, device="cuda", dtype=torch.float16, generator=gen)
+        b = torch.randn(GEMM_SIZE, GEMM_SIZE, device="cuda", dtype=torch.float16, generator=gen)
+        if name == "zeros":
+            a.zero_()
+            b.zero_()
+        c = torch.empty(GEMM_SIZE, GEMM_SIZE, device="cuda", dtype=torch.float16)
+        for _ in range(args.warmup):
+            torch.matmul(a, b, out=c)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            torch.matmul(a, b, out=c)
+        e1.record()
+        torch.cuda.synchronize()
+        avg = e0.elapsed_time(e1) / 1e3 / args.steps
+        tflops = 2 * GEMM_SIZE**3 / avg / 1e12
+        out[name] = {"us": round(avg * 1e6, 1), "tflops": round(tflops, 1),
+                     "frac": round(tflops / MI355X_FP16_DENSE_TFLOPS, 4)}
+        del a, b, c
+    print(json.dumps(out), flush=True)
+    return 0
+
+
 def run_single(entry, args):
     """Times one workload (used under rocprofv3); prints one JSON line."""
     if args.only == "copy":
         return run_copy_calibration(args)
+    if args.only == "gemm":
+        return run_gemm_ceiling(args)
     batch, heads, seq_len, sigma = WORKLOADS[args.only]
     modes = {"noncausal": (False,), "causal": (True,), "both": (False, True)}[args.mode]
     inputs = make_inputs(batch, heads, seq_len, sigma=sigma, device="cuda")
@@ -299,7 +338,7 @@ def main() -> int:
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--skip-north-star", action="store_true")
     parser.add_argument("--skip-cpu", action="store_true")
-    parser.add_argument("--only", choices=sorted(WORKLOADS) + ["copy"],
+    parser.add_argument("--only", choices=sorted(WORKLOADS) + ["copy", "gemm"],
                         help="time one workload only (for profilers); prints its own JSON line")
     parser.add_argument("--mode", choices=("noncausal", "causal", "both"), default="both")
     args = parser.parse_args()

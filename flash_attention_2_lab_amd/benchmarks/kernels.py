@@ -83,8 +83,10 @@ class _CpuSdpa:
 
 KERNELS: list[KernelSpec] = [
     KernelSpec("naive_online", _entry("naive_attention_forward"), _simt_support((64, 128))),
-    # bfloat16 SDPA on the device is left out: torch's bf16 batched products with a
-    # transposed operand have faulted the GPU on this image.
+    # bfloat16 SDPA on the device is left out (the reference offers it for every
+    # workload, benchmarks/kernels.py:148-152): torch's bf16 batched products with a
+    # transposed right operand, which SDPA's math path issues, are listed by the GPU
+    # pool this runs on as faulting its GPUs. This harness has never run that call.
     KernelSpec("pytorch_sdpa", _sdpa, lambda w: w.dtype in (torch.float16, torch.float32)),
     KernelSpec("block_online", _entry("block_attention_forward"), _simt_support((64, 128))),
     KernelSpec("tiled_simt", _entry("tiled_attention_forward"), _simt_support((64,))),

@@ -45,7 +45,15 @@ enum fa2_status {
 /*
  * Fused attention forward, O = softmax(Q K^T / sqrt(64) [+ causal mask]) V.
  * FP16 in/out, FP32 accumulation and FP32 online softmax; P is rounded to FP16
- * before the P.V product, the softmax denominator uses FP32 probabilities.
+ * before the P.V product. The softmax denominator differs from the reference's FP32
+ * sum of unrounded probabilities in most kernels: they add the FP16-rounded P in
+ * pairs (an FP16 add) and accumulate the pair sums into FP32 with v_dot2, so that
+ * O is a convex combination of the P the product used. The causal kernel for 1024
+ * to 2047 keys on few heads (FA2_KERNEL_KEY_SPLIT_PAIRS16) sums unrounded FP32 P.
+ * Outputs stay within atol 2e-3 + rtol 1e-2 of the FP32 formula.
+ * NaN and +-inf inputs make NaN or inf exactly the outputs the FP32 formula does,
+ * except that a causal row i < j may or may not see a NaN or inf in value row j,
+ * where the formula's 0 * NaN always does.
  * causal != 0 masks key j > query i.
  *
  * Replaces tensorcore_attention_forward_production_128x128

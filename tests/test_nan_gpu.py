@@ -1,4 +1,4 @@
-"""NaN inputs on the GPU: which output rows the kernels make NaN, against the oracle.
+"""NaN and infinite inputs on the GPU: the output rows they make non-finite, against the oracle.
 
 The reference's FP32 formula (flash_attention/reference.py:46-59) propagates a NaN in
 Q, K or V through the scores, the softmax and P.V. The kernels are compiled with
@@ -14,6 +14,15 @@ One case is not covered: causal rows i < j with a NaN in value row j. The formul
 P.V multiplies their zero probability by the NaN (0 * NaN = NaN in every row of the
 head); the kernels skip key tiles past a row's diagonal, so such a row is NaN only when
 key j falls in a key tile its wave computes.
+
+Infinities are honoured (no -fno-honor-infs) and follow the formula the same way:
+* +inf in query row i gives that row scores of both signs of infinity; its max is +inf
+  and inf - inf makes the row NaN;
+* +inf in key row j, dimension e, gives +inf scores in the rows whose q[e] > 0 (NaN
+  rows) and -inf in the rows whose q[e] < 0 (key j gets probability 0, the row stays
+  finite);
+* +inf in value (j, d) makes dimension d infinite in every row that sees key j, with
+  the same exception as the NaN case for causal rows i < j.
 """
 
 from __future__ import annotations
@@ -96,3 +105,58 @@ def test_nan_in_value_element(shape, causal, kernel):
     mask[b, h, j if causal else 0:, d] = True
     assert torch.equal(torch.isnan(expected), mask)
     _check(out, expected, mask)
+
+
+def _check_nonfinite(out, expected):
+    """NaN and +-inf exactly where the oracle has them; elsewhere within the gate."""
+    out = out.float().cpu()
+    assert torch.equal(torch.isnan(out), torch.isnan(expected))
+    assert torch.equal(torch.isposinf(out), torch.isposinf(expected))
+    assert torch.equal(torch.isneginf(out), torch.isneginf(expected))
+    finite = torch.isfinite(expected)
+    torch.testing.assert_close(out[finite], expected[finite], atol=2e-3, rtol=1e-2)
+
+
+@pytest.mark.parametrize("shape, causal, kernel", SHAPES, ids=IDS)
+def test_inf_in_query_row(shape, causal, kernel):
+    assert capi.forward_plan(*shape, causal) == kernel
+    q, k, v = _inputs(shape, seed=74)
+    n = shape[2]
+    b, h, i = shape[0] - 1, 0, n - 3
+    q[b, h, i, 17] = float("inf")
+    expected = attention_reference_fp32(q, k, v, causal=causal)
+    assert torch.isnan(expected[b, h, i]).all() and int(torch.isnan(expected).sum()) == 64
+    _check_nonfinite(ENTRY(q.cuda(), k.cuda(), v.cuda(), causal), expected)
+
+
+@pytest.mark.parametrize("shape, causal, kernel", SHAPES, ids=IDS)
+def test_inf_in_key_row(shape, causal, kernel):
+    assert capi.forward_plan(*shape, causal) == kernel
+    q, k, v = _inputs(shape, seed=75)
+    n = shape[2]
+    b, h, j, e = 0, shape[1] // 3, n // 4 + 1, 40
+    k[b, h, j, e] = float("inf")
+    expected = attention_reference_fp32(q, k, v, causal=causal)
+    nan_rows = q[b, h, :, e].float() > 0
+    if causal:
+        nan_rows[:j] = False
+    assert torch.equal(torch.isnan(expected[b, h]).all(-1), nan_rows)
+    assert 0 < int(nan_rows.sum()) < n - j
+    _check_nonfinite(ENTRY(q.cuda(), k.cuda(), v.cuda(), causal), expected)
+
+
+@pytest.mark.parametrize("shape, causal, kernel", SHAPES, ids=IDS)
+def test_inf_in_value_element(shape, causal, kernel):
+    assert capi.forward_plan(*shape, causal) == kernel
+    q, k, v = _inputs(shape, seed=76)
+    n = shape[2]
+    b, h, j, d = shape[0] - 1, shape[1] - 1, 33, 50
+    v[b, h, j, d] = float("inf")
+    expected = attention_reference_fp32(q, k, v, causal=causal)
+    out = ENTRY(q.cuda(), k.cuda(), v.cuda(), causal).float().cpu()
+    if causal:
+        # Rows before the key: compared outside dimension d only (see the module docstring).
+        out[b, h, :j, d] = 0.0
+        expected[b, h, :j, d] = 0.0
+    assert int(torch.isinf(expected).sum()) == n - (j if causal else 0)
+    _check_nonfinite(out, expected)

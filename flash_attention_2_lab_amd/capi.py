@@ -37,6 +37,7 @@ FA2_KERNEL_KEY_SPLIT_64 = 4
 FA2_KERNEL_KEY_SPLIT_32 = 5
 FA2_KERNEL_KEY_SPLIT_8_WAVES = 6
 FA2_KERNEL_KEY_SPLIT_PAIRS16 = 7
+FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES = 8
 
 
 class Fa2Error(RuntimeError):

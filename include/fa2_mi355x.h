@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define FA2_MI355X_ABI_VERSION 5
+#define FA2_MI355X_ABI_VERSION 6
 
 enum fa2_status {
     FA2_STATUS_SUCCESS = 0,
@@ -141,8 +141,10 @@ enum fa2_forward_kernel {
                                      /* 64-key tiles                                       */
     FA2_KERNEL_KEY_SPLIT_32 = 5,     /* the same with 32-key tiles                         */
     FA2_KERNEL_KEY_SPLIT_8_WAVES = 6, /* keys split over 8 waves, 32-key tiles             */
-    FA2_KERNEL_KEY_SPLIT_PAIRS16 = 7  /* causal: 16-query blocks p and N/16-1-p of a head  */
+    FA2_KERNEL_KEY_SPLIT_PAIRS16 = 7, /* causal: 16-query blocks p and N/16-1-p of a head  */
                                       /* per workgroup, keys split over 4 waves            */
+    FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES = 8 /* as KEY_SPLIT_64, plus 4 waves that only fetch */
+                                          /* K/V tiles into LDS for the 4 computing waves  */
 };
 
 /*

@@ -122,7 +122,7 @@ int main(void) {
                 for (int causal = 0; causal <= 1; ++causal) {
                     const int64_t batch = counts[a], heads = counts[b], n = sizes[c];
                     const int plan = fa2_forward_plan(batch, heads, n, causal);
-                    CHECK(plan >= FA2_KERNEL_NONE && plan <= FA2_KERNEL_KEY_SPLIT_PAIRS16, "plan %d", plan);
+                    CHECK(plan >= FA2_KERNEL_NONE && plan <= FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES, "plan %d", plan);
                     int none = batch <= 0 || heads <= 0 || n <= 0 || n > ((int64_t)1 << 24);
                     if (!none) none = batch > (int64_t)UINT32_MAX / heads;
                     if (!none) none = batch * heads > (int64_t)UINT32_MAX / ((n + 31) / 32);
@@ -170,7 +170,8 @@ int main(void) {
     CHECK(fa2_matmul_16x64x16_f16(fake[0], NULL, fo, 1, NULL) == FA2_STATUS_NULL_POINTER, "matmul null");
     CHECK(fa2_matmul_16x64x16_f16(fake[0] + 1, fake[1], fo, 1, NULL) == FA2_STATUS_MISALIGNED, "matmul misaligned");
 
-    CHECK(fa2_forward_plan(1, 8, 1024, 0) == FA2_KERNEL_KEY_SPLIT_64, "plan bench size");
+    CHECK(fa2_forward_plan(1, 8, 1024, 0) == FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES, "plan bench size");
+    CHECK(fa2_forward_plan(1, 8, 896, 0) == FA2_KERNEL_KEY_SPLIT_64, "plan below 1024 keys");
     CHECK(fa2_forward_plan(16, 16, 4096, 0) == FA2_KERNEL_256_QUERY, "plan throughput size");
     CHECK(fa2_forward_plan(16, 16, 4096, 1) == FA2_KERNEL_256_QUERY, "plan throughput size causal");
     CHECK(fa2_forward_plan(16, 16, 1024, 1) == FA2_KERNEL_256_QUERY_PAIRS, "plan causal pairs");

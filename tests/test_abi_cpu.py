@@ -39,7 +39,7 @@ def test_status_codes_match_header():
 def test_kernel_ids_match_header():
     text = capi.HEADER_PATH.read_text()
     for name in ("NONE", "256_QUERY", "256_QUERY_PAIRS", "128_QUERY", "KEY_SPLIT_64", "KEY_SPLIT_32",
-                 "KEY_SPLIT_8_WAVES", "KEY_SPLIT_PAIRS16"):
+                 "KEY_SPLIT_8_WAVES", "KEY_SPLIT_PAIRS16", "KEY_SPLIT_64_DMA_WAVES"):
         value = int(re.search(rf"FA2_KERNEL_{name} = (\d+)", text).group(1))
         assert getattr(capi, f"FA2_KERNEL_{name}") == value
 
@@ -49,10 +49,11 @@ K = capi
 
 @pytest.mark.parametrize("batch, heads, seq_len, causal, kernel", [
     # Noncausal: 256-query from 512 groups of 256 queries, 128-query from 256 groups of
-    # 128, key-split below (64-key tiles up to 256 blocks of 32 queries).
+    # 128, key-split below (64-key tiles up to 256 blocks of 32 queries; from 1024 keys
+    # with separate DMA waves).
     (1, 128, 1024, False, K.FA2_KERNEL_256_QUERY), (1, 127, 1024, False, K.FA2_KERNEL_128_QUERY),
     (16, 16, 4096, False, K.FA2_KERNEL_256_QUERY), (1, 32, 1024, False, K.FA2_KERNEL_128_QUERY),
-    (1, 31, 1024, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 8, 1024, False, K.FA2_KERNEL_KEY_SPLIT_64),
+    (1, 31, 1024, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 8, 1024, False, K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES),
     (1, 9, 1024, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 8, 128, False, K.FA2_KERNEL_KEY_SPLIT_64),
     # Causal: 256-query from 512 workgroups of tile pairs when a head has an even
     # number T of tiles, single tiles from 2048 with an odd number. Single tiles in
@@ -71,7 +72,9 @@ K = capi
     # Key-split shapes from 2048 keys on split each block's keys over 8 waves.
     (1, 2, 4096, False, K.FA2_KERNEL_KEY_SPLIT_8_WAVES), (1, 1, 2048, True, K.FA2_KERNEL_KEY_SPLIT_8_WAVES),
     (1, 4, 2048, False, K.FA2_KERNEL_KEY_SPLIT_8_WAVES), (1, 1, 8192, True, K.FA2_KERNEL_KEY_SPLIT_8_WAVES),
-    (1, 4, 1024, False, K.FA2_KERNEL_KEY_SPLIT_64), (1, 8, 2048, True, K.FA2_KERNEL_KEY_SPLIT_32),
+    (1, 4, 1024, False, K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES), (1, 8, 2048, True, K.FA2_KERNEL_KEY_SPLIT_32),
+    (1, 8, 896, False, K.FA2_KERNEL_KEY_SPLIT_64), (1, 4, 1920, False, K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES),
+    (1, 4, 1040, False, K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES), (1, 2, 2000, False, K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES),
     (1, 1, 2064, False, K.FA2_KERNEL_KEY_SPLIT_8_WAVES),
     # Sequence lengths the production entry rejects but the Bc16/Bc32 entries take
     # (partial last block) run the key-split kernel.

@@ -255,16 +255,18 @@ def test_long_single_head_n2pow20(causal):
 
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("shape", [(1, 64, 1024), (1, 8, 1024), (1, 9, 1024), (3, 3, 1024), (1, 4, 2048),
-                                   (1, 2, 4096)])
+                                   (1, 2, 4096), (1, 8, 768)])
 def test_growing_scores_match_oracle(shape, causal):
     # Key norms ramp up 12x along the sequence, so the running max keeps growing (by
     # some 50 log2 units over a row) and the kernels' stale-max probabilities overflow
     # the 2^14 tile-sum bound several times per row: exercises the exact-max
     # recompute path of the 128-query kernel and of every key-split variant (64-key
-    # tiles; 32-key tiles; 8 waves; causal pairs of 16-query blocks).
+    # tiles, with and without DMA waves; 32-key tiles; 8 waves; causal pairs of
+    # 16-query blocks).
     assert capi.forward_plan(*shape, causal) in (
         capi.FA2_KERNEL_128_QUERY, capi.FA2_KERNEL_KEY_SPLIT_64, capi.FA2_KERNEL_KEY_SPLIT_32,
-        capi.FA2_KERNEL_KEY_SPLIT_8_WAVES, capi.FA2_KERNEL_KEY_SPLIT_PAIRS16)
+        capi.FA2_KERNEL_KEY_SPLIT_8_WAVES, capi.FA2_KERNEL_KEY_SPLIT_PAIRS16,
+        capi.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES)
     q, k, v = _inputs(*shape, seed=9)
     ramp = torch.linspace(1.0, 12.0, shape[2]).view(1, 1, -1, 1)
     k = (k.float() * ramp).half()
@@ -273,14 +275,15 @@ def test_growing_scores_match_oracle(shape, causal):
     _assert_close_to_oracle(out, attention_reference_fp32(q, k, v, causal=causal))
 
 
-@pytest.mark.parametrize("shape", [(1, 4, 2000), (1, 2, 2064)])
+@pytest.mark.parametrize("shape", [(1, 4, 2000), (1, 2, 2064), (1, 4, 880)])
 def test_growing_scores_on_partial_key_tiles(shape):
     # The partial-tile key-split instantiations (sequence lengths that are multiples of
-    # 16 only, through the Bc16 entry): 64-key tiles below 2048 keys, 8 waves with
-    # 32-key tiles from 2048 on, keys masked past the end. Ramped key norms force the
-    # exact-max recompute on the partial tiles too.
+    # 16 only, through the Bc16 entry): 64-key tiles below 1024 keys, with DMA waves
+    # from 1024, 8 waves with 32-key tiles from 2048 on, keys masked past the end.
+    # Ramped key norms force the exact-max recompute on the partial tiles too.
     batch, heads, seq_len = shape
     assert capi.forward_plan(batch, heads, seq_len, False) in (capi.FA2_KERNEL_KEY_SPLIT_64,
+                                                               capi.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES,
                                                                capi.FA2_KERNEL_KEY_SPLIT_8_WAVES)
     q, k, v = _inputs(batch, heads, seq_len, seed=19)
     k = (k.float() * torch.linspace(1.0, 12.0, seq_len).view(1, 1, -1, 1)).half()

@@ -34,7 +34,10 @@ CASES = [
     (1, 128, 1024, False, "256-query (512 groups of 256)", K.FA2_KERNEL_256_QUERY),
     (1, 31, 1024, False, "key-split, 32-key tiles (248 groups of 128)", K.FA2_KERNEL_KEY_SPLIT_32),
     (1, 32, 1024, False, "128-query (256 groups of 128)", K.FA2_KERNEL_128_QUERY),
-    (1, 8, 1024, False, "key-split, 64-key tiles (256 query blocks)", K.FA2_KERNEL_KEY_SPLIT_64),
+    (1, 8, 1024, False, "key-split, 64-key tiles, DMA waves (256 query blocks)", K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES),
+    (1, 8, 896, False, "key-split, 64-key tiles (224 blocks below 1024 keys)", K.FA2_KERNEL_KEY_SPLIT_64),
+    (1, 4, 1920, False, "key-split, 64-key tiles, DMA waves (the longest below 2048 keys)",
+     K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES),
     (1, 9, 1024, False, "key-split, 32-key tiles (288 query blocks)", K.FA2_KERNEL_KEY_SPLIT_32),
     (1, 255, 1024, True, "128-query (510 tile pairs)", K.FA2_KERNEL_128_QUERY),
     (1, 256, 1024, True, "256-query, tile pairs (512 pairs)", K.FA2_KERNEL_256_QUERY_PAIRS),
@@ -48,7 +51,7 @@ CASES = [
     (1, 8, 896, True, "key-split, 64-key tiles (224 blocks below 1024 keys)", K.FA2_KERNEL_KEY_SPLIT_64),
     (1, 2, 1024, True, "key-split, pairs of 16-query blocks (64 pairs)", K.FA2_KERNEL_KEY_SPLIT_PAIRS16),
     (3, 3, 1024, True, "key-split, 32-key tiles (288 query blocks)", K.FA2_KERNEL_KEY_SPLIT_32),
-    (1, 4, 1024, False, "key-split, 64-key tiles (1024 keys)", K.FA2_KERNEL_KEY_SPLIT_64),
+    (1, 4, 1024, False, "key-split, 64-key tiles, DMA waves (1024 keys)", K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES),
     (1, 4, 2048, False, "key-split, 8 waves (2048 keys, 256 query blocks)", K.FA2_KERNEL_KEY_SPLIT_8_WAVES),
     (1, 2, 4096, True, "key-split, 8 waves (4096 keys)", K.FA2_KERNEL_KEY_SPLIT_8_WAVES),
     (1, 8, 2048, True, "key-split, 32-key tiles (512 query blocks of 2048 keys)", K.FA2_KERNEL_KEY_SPLIT_32),

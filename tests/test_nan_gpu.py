@@ -39,7 +39,8 @@ pytestmark = pytest.mark.gpu
 ENTRY = fa.flash_attention_cuda.tensorcore_attention_forward_production_128x128
 
 SHAPES = [
-    ((1, 8, 1024), False, capi.FA2_KERNEL_KEY_SPLIT_64), ((1, 8, 1024), True, capi.FA2_KERNEL_KEY_SPLIT_PAIRS16),
+    ((1, 8, 1024), False, capi.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES), ((1, 8, 1024), True, capi.FA2_KERNEL_KEY_SPLIT_PAIRS16),
+    ((1, 8, 768), False, capi.FA2_KERNEL_KEY_SPLIT_64),
     ((1, 64, 1024), False, capi.FA2_KERNEL_128_QUERY), ((1, 64, 1024), True, capi.FA2_KERNEL_128_QUERY),
     ((8, 16, 1024), False, capi.FA2_KERNEL_256_QUERY), ((8, 64, 1024), True, capi.FA2_KERNEL_256_QUERY),
     ((8, 64, 512), True, capi.FA2_KERNEL_256_QUERY_PAIRS), ((1, 4, 2048), False, capi.FA2_KERNEL_KEY_SPLIT_8_WAVES),

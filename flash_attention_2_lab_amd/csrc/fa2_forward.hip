@@ -589,7 +589,9 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
 // of their own (each wave fetches and reads only its own stages, so the key loop
 // has no workgroup barrier), and keep their own running max, sum and O. At the end
 // the partial results are merged through LDS:
-//   m = max_w m_w,  l = sum_w l_w 2^((m_w - m) s log2e),  O = sum_w O_w 2^(...) / l.
+//   m = max_w m_w,  l = sum_w l_w 2^((m_w - m) s log2e),  O = sum_w O_w 2^(...) / l,
+// and the FP16 output tile is staged in LDS so that the stores write whole 128-byte rows
+// (measured 0-2% faster than 8-byte stores scattered over the 32 rows).
 template <bool kCausal, bool kPartial, int kSplit, int kBlocks>
 __global__ __launch_bounds__(kSplit * 64) void fa2_forward_splitk_kernel(const _Float16* __restrict__ query,
                                                                  const _Float16* __restrict__ key,
@@ -847,10 +849,11 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_splitk_kernel(const _
         weight[w] = m_w == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_w - m_tot) * scale_log2);
         l_tot += red_l[w * 64 + lane] * weight[w];
     }
-    if (kPartial && !query_valid) return;
     const float inv_l = 1.0f / l_tot;
-    _Float16* o_row = o_head + (size_t)my_query * kHeadDim;
-    // Wave w writes float groups j = w, w + kSplit, ... of the 8.
+    // The block's FP16 output tile goes through LDS (past the merge area): float group j
+    // of row lq is 16-byte chunk j of the row, XOR-swizzled by the row; then the waves
+    // store whole 128-byte rows, one 16-byte chunk per lane (32 / kSplit rows per wave).
+    uint8_t* const out_lds = smem + kMergeBytes;
 #pragma unroll
     for (int j0 = 0; j0 < 8; j0 += kSplit) {
         const int j = j0 + wave;
@@ -861,12 +864,20 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_splitk_kernel(const _
             const f32x4 v = *reinterpret_cast<const f32x4*>(red_o + ((w * 8 + j) * 64 + lane) * 4);
             acc += v * weight[w];
         }
-        // Float j holds dims 32*(j/4) + 8*(j%4) + 4*half + 0..3 of my_query.
+        // Float j holds dims 32*(j/4) + 8*(j%4) + 4*half + 0..3 of my_query: chunk j, half `half`.
         const f16x2 a = pack_rn(acc[0] * inv_l, acc[1] * inv_l);
         const f16x2 c = pack_rn(acc[2] * inv_l, acc[3] * inv_l);
-        *reinterpret_cast<f16x4*>(o_row + 32 * (j >> 2) + 8 * (j & 3) + 4 * half) =
+        *reinterpret_cast<f16x4*>(out_lds + lq * kRowBytes + ((j ^ (lq & 7)) << 4) + 8 * half) =
             __builtin_shufflevector(a, c, 0, 1, 2, 3);
     }
+    __syncthreads();
+    constexpr int kRowsPerWave = kQueriesPerWave / kSplit;
+    if ((lane >> 3) >= kRowsPerWave) return;
+    const int out_row = kRowsPerWave * wave + (lane >> 3);
+    const int chunk = lane & 7;
+    const f16x8 row_chunk = *reinterpret_cast<const f16x8*>(out_lds + out_row * kRowBytes + ((chunk ^ (out_row & 7)) << 4));
+    if (kPartial && q0 + out_row >= seq_len) return;
+    *reinterpret_cast<f16x8*>(o_head + (size_t)(q0 + out_row) * kHeadDim + 8 * chunk) = row_chunk;
 }
 
 // Key-split kernel with dedicated DMA waves. A CU fills its LDS from L2 at about 64 B
@@ -898,6 +909,8 @@ __global__ __launch_bounds__(2 * kSplit * 64) void fa2_forward_splitk_dma_waves_
     constexpr int kQBytes = kQueriesPerWave * kRowBytes;     // one copy of the block's Q rows
     constexpr int kRingBytes = kSplit * 2 * kStageBytes;
     constexpr int kSmemBytes = kRingBytes + kQBytes > kMergeBytes ? kRingBytes + kQBytes : kMergeBytes;
+    static_assert(kSplit == 4, "the epilogue stores 8 rows per consumer wave");
+    static_assert(kMergeBytes + kQueriesPerWave * kRowBytes <= kSmemBytes, "output tile past the merge area");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmemBytes];
 
     const int tid = threadIdx.x;
@@ -974,6 +987,7 @@ __global__ __launch_bounds__(2 * kSplit * 64) void fa2_forward_splitk_dma_waves_
             if (j + 2 < n_tiles) dma_tile(t_begin + j + 2, j & 1);
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
         __syncthreads();
         __syncthreads();
         return;
@@ -1138,9 +1152,11 @@ __global__ __launch_bounds__(2 * kSplit * 64) void fa2_forward_splitk_dma_waves_
         weight[w] = m_w == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_w - m_tot) * scale_log2);
         l_tot += red_l[w * 64 + lane] * weight[w];
     }
-    if (kPartial && !query_valid) return;
     const float inv_l = 1.0f / l_tot;
-    _Float16* o_row = o_head + (size_t)my_query * kHeadDim;
+    // The block's FP16 output tile goes through LDS (past the merge area): float group j
+    // of row lq is 16-byte chunk j of the row, XOR-swizzled by the row; then wave w
+    // stores rows 8w..8w+7 as whole 128-byte rows, one 16-byte chunk per lane.
+    uint8_t* const out_lds = smem + kMergeBytes;
 #pragma unroll
     for (int j0 = 0; j0 < 8; j0 += kSplit) {
         const int j = j0 + cw;
@@ -1151,11 +1167,18 @@ __global__ __launch_bounds__(2 * kSplit * 64) void fa2_forward_splitk_dma_waves_
             const f32x4 v = *reinterpret_cast<const f32x4*>(red_o + ((w * 8 + j) * 64 + lane) * 4);
             acc += v * weight[w];
         }
+        // Float j holds dims 32*(j/4) + 8*(j%4) + 4*half + 0..3 of my_query: chunk j, half `half`.
         const f16x2 a = pack_rn(acc[0] * inv_l, acc[1] * inv_l);
         const f16x2 c = pack_rn(acc[2] * inv_l, acc[3] * inv_l);
-        *reinterpret_cast<f16x4*>(o_row + 32 * (j >> 2) + 8 * (j & 3) + 4 * half) =
+        *reinterpret_cast<f16x4*>(out_lds + lq * kRowBytes + ((j ^ (lq & 7)) << 4) + 8 * half) =
             __builtin_shufflevector(a, c, 0, 1, 2, 3);
     }
+    __syncthreads();
+    const int out_row = 8 * cw + (lane >> 3);
+    const int chunk = lane & 7;
+    const f16x8 row_chunk = *reinterpret_cast<const f16x8*>(out_lds + out_row * kRowBytes + ((chunk ^ (out_row & 7)) << 4));
+    if (kPartial && q0 + out_row >= seq_len) return;
+    *reinterpret_cast<f16x8*>(o_head + (size_t)(q0 + out_row) * kHeadDim + 8 * chunk) = row_chunk;
 }
 
 // Key order of a 16-key MFMA block in the paired 16-query kernel: group g of 4 rows
@@ -1451,18 +1474,29 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_pairs16_kernel(const 
         l_tot += l_w * weight[w];
     }
     const float inv_l = 1.0f / l_tot;
-    _Float16* o_row = o_head + (size_t)(q0[b] + lq) * kHeadDim;
+    // Both blocks' FP16 output rows go through LDS (past the merge area): row lq of block
+    // b, 16-byte chunk c at (c ^ (row & 7)); then wave w stores 32 / kSplit whole rows.
+    uint8_t* const out_lds = smem + kMergeBytes;
 #pragma unroll
     for (int x = 0; x < kDblkPerWave; ++x) {
         const int dblk = dblk0 + x;
         f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int w = 0; w < kSplit; ++w) acc += red_o[((b * kSplit + w) * 4 + dblk) * 64 + lane] * weight[w];
-        // Lane holds dims 16dblk + 4grp + 0..3 of query q0 + lq.
+        // Lane holds dims 16dblk + 4grp + 0..3 of query q0 + lq: chunk 2dblk + grp/2, half grp%2.
         const f16x2 lo = pack_rn(acc[0] * inv_l, acc[1] * inv_l);
         const f16x2 hi = pack_rn(acc[2] * inv_l, acc[3] * inv_l);
-        *reinterpret_cast<f16x4*>(o_row + 16 * dblk + 4 * grp) = __builtin_shufflevector(lo, hi, 0, 1, 2, 3);
+        const int row = 16 * b + lq;
+        *reinterpret_cast<f16x4*>(out_lds + row * kRowBytes + (((2 * dblk + (grp >> 1)) ^ (row & 7)) << 4) + 8 * (grp & 1)) =
+            __builtin_shufflevector(lo, hi, 0, 1, 2, 3);
     }
+    __syncthreads();
+    constexpr int kRowsPerWave = 32 / kSplit;
+    if ((lane >> 3) >= kRowsPerWave) return;
+    const int out_row = kRowsPerWave * wave + (lane >> 3);  // 0..15 block 0, 16..31 block 1
+    const int chunk = lane & 7;
+    const f16x8 row_chunk = *reinterpret_cast<const f16x8*>(out_lds + out_row * kRowBytes + ((chunk ^ (out_row & 7)) << 4));
+    *reinterpret_cast<f16x8*>(o_head + (size_t)(q0[out_row >> 4] + (out_row & 15)) * kHeadDim + 8 * chunk) = row_chunk;
 }
 
 // Wide variant: 64 queries per wave, as two 32-query blocks (a: q_wave + 0..31,

@@ -526,18 +526,28 @@ void fa2_forward_d64_kernel(const _Float16* __restrict__ query,
     }
 
     // Epilogue: O = O^T / l. Accumulator i of d-block dblk holds dim
-    // 32*dblk + 8*(i/4) + 4*half + i%4 of my_query.
+    // 32*dblk + 8*(i/4) + 4*half + i%4 of my_query, i.e. 16-byte chunk 4*dblk + i/4 of
+    // its row. The wave's 32 rows go through its 4 KiB of stage 3 (free after the last
+    // tile's barrier; chunk c of row r at c ^ (r & 7)) and are stored as whole rows.
     const float inv_l = 1.0f / sum_across_halves(l_run);
-    _Float16* o_row = o_head + (size_t)my_query * kHeadDim;
+    uint8_t* const out_lds = stage3 + wave * 4096;
 #pragma unroll
     for (int dblk = 0; dblk < 2; ++dblk)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const f16x2 a = pack_rn(o_acc[dblk][4 * g + 0] * inv_l, o_acc[dblk][4 * g + 1] * inv_l);
             const f16x2 c = pack_rn(o_acc[dblk][4 * g + 2] * inv_l, o_acc[dblk][4 * g + 3] * inv_l);
-            *reinterpret_cast<f16x4*>(o_row + 32 * dblk + 8 * g + 4 * half) =
+            const int chunk = 4 * dblk + g;
+            *reinterpret_cast<f16x4*>(out_lds + lq * kRowBytes + ((chunk ^ (lq & 7)) << 4) + 8 * half) =
                 __builtin_shufflevector(a, c, 0, 1, 2, 3);
         }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int row = 8 * r + (lane >> 3);
+        const int chunk = lane & 7;
+        const f16x8 v = *reinterpret_cast<const f16x8*>(out_lds + row * kRowBytes + ((chunk ^ (row & 7)) << 4));
+        *reinterpret_cast<f16x8*>(o_head + (size_t)(q_wave + row) * kHeadDim + 8 * chunk) = v;
+    }
 }
 
 // LDS-DMA through inline assembly: M0 = LDS destination of lane 0 (wave-uniform),
@@ -1676,18 +1686,34 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
 
     // Epilogue of a pass: O = O^T / l. Accumulator i of d-block dblk holds dim
     // 32*dblk + 8*(i/4) + 4*half + i%4 of the lane's query.
+    // Staged through this wave's 4 KiB of stage 3 (free after the last tile's barrier; the
+    // next pass's prologue fetches into stages 0..2): chunk c of row r at c ^ (r & 7).
     auto store = [&](const f32x16 (&o)[2], float l_run, int q) {
         const float inv_l = 1.0f / sum_across_halves(l_run);
-        const int row = q * kRowBytes + 8 * half;
+        // The lane index recomputed here, so that nothing but the accumulators stays live
+        // across the key loop for this epilogue (the causal kernels use all 256 VGPRs).
+        int lane_o = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+        asm volatile("" : "+v"(lane_o));
+        const int lq = lane_o & 31, half = lane_o >> 5;
+        uint8_t* const out_lds = smem + 3 * kStageBytes + wave * 4096;
 #pragma unroll
         for (int dblk = 0; dblk < 2; ++dblk)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const f16x2 a = pack_rn(o[dblk][4 * g + 0] * inv_l, o[dblk][4 * g + 1] * inv_l);
                 const f16x2 c = pack_rn(o[dblk][4 * g + 2] * inv_l, o[dblk][4 * g + 3] * inv_l);
-                const f16x4 v = __builtin_shufflevector(a, c, 0, 1, 2, 3);
-                __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), o_head, row + 64 * dblk + 16 * g, 0, 0);
+                const int chunk = 4 * dblk + g;
+                *reinterpret_cast<f16x4*>(out_lds + lq * kRowBytes + ((chunk ^ (lq & 7)) << 4) + 8 * half) =
+                    __builtin_shufflevector(a, c, 0, 1, 2, 3);
             }
+        const int q_row0 = q - lq;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 8 * r + (lane_o >> 3);
+            const int chunk = lane_o & 7;
+            const f16x8 v = *reinterpret_cast<const f16x8*>(out_lds + row * kRowBytes + ((chunk ^ (row & 7)) << 4));
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), o_head, (q_row0 + row) * kRowBytes + 16 * chunk, 0, 0);
+        }
     };
 
 #pragma unroll

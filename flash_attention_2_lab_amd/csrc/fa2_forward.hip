@@ -1211,10 +1211,12 @@ __device__ __forceinline__ float max_across_groups16(float x) {
 // (16 queries) sees 16(b+1) keys, so one block per workgroup leaves the workgroup of
 // the last block with all the keys and the first with a handful. Here a workgroup
 // runs block NB-1-p (heavy) and block p (light) of one head (NB = seq_len / 16), so
-// every workgroup has the same ceil((NB-p)/4) + ceil((p+1)/4) key tiles of 64 (17 at
-// seq_len 1024): half the work of a noncausal 32-query workgroup, in the same grid.
-// The workgroup's tiles (the heavy block's, then the light block's) are split into
-// kSplit contiguous shares, one per wave; a wave streams its share through two LDS
+// every workgroup has the same ceil((NB-p)/4) + ceil((p+1)/4) block-tiles of 64 keys
+// (17 at seq_len 1024): half the work of a noncausal 32-query workgroup, in the same
+// grid. The light block's tiles are the first of the heavy block's, and each is
+// fetched and read from LDS once for both blocks. The workgroup's key tiles are split
+// into kSplit contiguous shares, one per wave, balanced by cost (a tile for both blocks
+// counts 4, one for the heavy block 3); a wave streams its share through two LDS
 // stages of its own, keeps a running max, sum and O per block, and the partial
 // results of each block are merged through LDS at the end. Scores come from
 // v_mfma_f32_16x16x32_f16 (S^T = K Q^T, 16 keys x 16 queries per MFMA): lane l holds
@@ -1267,9 +1269,21 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_pairs16_kernel(const 
     const int q0[2] = {(blocks_per_head - 1 - pair) * kBlockQ, pair * kBlockQ};
     const int tiles0 = (q0[0] + kBlockQ + kKeysPerTile - 1) / kKeysPerTile;
     const int tiles1 = (q0[1] + kBlockQ + kKeysPerTile - 1) / kKeysPerTile;
-    const int total = tiles0 + tiles1;
-    const int t_begin = wave * total / kSplit;
-    const int t_end = (wave + 1) * total / kSplit;
+    // The light block's key tiles 0..tiles1-1 are a subset of the heavy block's
+    // 0..tiles0-1: tile i < tiles1 is fetched once and computed for both blocks, the
+    // others for the heavy block only. Wave w takes a contiguous range of tiles with about
+    // 1/kSplit of the cost, counting a tile for both blocks as 4 and one for the heavy
+    // block as 3 (the fetch and K/V reads are shared). Measured on MI355X against the
+    // block-tile split (17 items over 4 waves at seq_len 1024): -8% at B1 H8 N1024 and
+    // B1 H2 N1024, -4% to -7% at 1280-1920 keys; 4:3 was 2-6% faster than 3:2 from
+    // 1280 keys on and equal at 1024.
+    const int total_cost = 4 * tiles1 + 3 * (tiles0 - tiles1);
+    auto split_at = [&](int w) -> int {
+        const int target = (w * total_cost + kSplit / 2) / kSplit;
+        return target <= 4 * tiles1 ? (target + 3) / 4 : tiles1 + (target - 4 * tiles1 + 2) / 3;
+    };
+    const int t_begin = split_at(wave);
+    const int t_end = split_at(wave + 1);
 
     uint8_t* const my_stages = smem + wave * kWaveBytes;
     const uint32_t my_stages_addr = lds_address(my_stages);
@@ -1289,9 +1303,7 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_pairs16_kernel(const 
             const int q_lane_off = perm16_inverse(lds_row) * kRowBytes + (((lane & 7) ^ tile_swizzle(lds_row)) << 4);
             dma16_asm(q_desc, my_q_addr + (uint32_t)(b * kQBlockBytes + n * 1024), q_lane_off, q0[b] * kRowBytes);
         }
-    // Item j of the workgroup's list: key tile j of block 0, then key tile j - tiles0 of block 1.
-    auto dma_item = [&](int j, int st) {
-        const int t = j < tiles0 ? j : j - tiles0;
+    auto dma_tile = [&](int t, int st) {
 #pragma unroll
         for (int n = 0; n < kDmaPerTile; ++n) {
             const int m = n / 8;
@@ -1301,7 +1313,7 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_pairs16_kernel(const 
                       dma_off[(r0 >> 3) & 1], t * kTileBytes + r0 * kRowBytes);
         }
     };
-    if (t_begin < t_end) dma_item(t_begin, 0);
+    if (t_begin < t_end) dma_tile(t_begin, 0);
 
     // Per-lane LDS offsets. K (A operand of S^T = K Q^T): MFMA row lq of a 16-key block
     // reads key row perm16(lq), dims 32ks + 8grp..+7 (chunk 4ks + grp). perm16 moves
@@ -1309,9 +1321,9 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_pairs16_kernel(const 
     // grp holds the 4 consecutive keys 4 tau(grp) + 0..3 of each 16 and the V transpose
     // reads stay 4-row reads; the order makes the 8 rows of every K read pass differ
     // in bit 3 and the 8 rows of every V transpose pass differ in bit 2, which the
-    // swizzle maps to distinct banks (measured: 10k bank conflicts per launch at
-    // B1 H8 N1024 causal against 149k in natural order). Q (B operand): query lq, stored
-    // at LDS row perm16(lq) by the DMA above, so its reads spread the same way.
+    // swizzle maps to distinct banks (measured: no bank conflicts at B1 H8 N1024 causal
+    // against 149k per launch in natural order). Q (B operand): query lq, stored at LDS
+    // row perm16(lq) by the DMA above, so its reads spread the same way.
     const int key_grp = perm16_group(grp);
     const int k_row = perm16(lq);
     const int swz_k = tile_swizzle(k_row);
@@ -1336,117 +1348,129 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_pairs16_kernel(const 
     for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int d = 0; d < 4; ++d) o[b][d] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    f16x8 qf[2][2];
 
-    // Items [t_begin, t_end) in order; block 0's, then block 1's. Scores S[kb][h]:
-    // keys 32kb + 16h + 4key_grp + 0..3 of the tile, query q0 + lq.
-    auto run_block = [&](auto block_tag, int j_begin, int j_end) {
+    // Block b's scores of tile t from the K fragments in registers, softmax, and P.V
+    // with the V fragments. S[kb][h]: keys 32kb + 16h + 4key_grp + 0..3, query q0[b] + lq.
+    auto block_tile = [&](auto block_tag, int t, bool first, const f16x8 (&kf)[2][2][2], const f16x8 (&vf)[2][4]) {
         constexpr int b = decltype(block_tag)::value;
-        f16x8 qf[2];
-        for (int j = j_begin; j < j_end; ++j) {
-            const int st = (j - t_begin) & 1;
-            if (j + 1 < t_end) {
-                dma_item(j + 1, st ^ 1);
-                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerTile) : "memory");  // tile j (and Q) landed
-            } else {
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        f32x4 s[2][2];
+        const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                s[kb][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[kb][h][0], qf[b][0], zero, 0, 0, 0);
+                s[kb][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[kb][h][1], qf[b][1], s[kb][h], 0, 0, 0);
             }
-            if (j == j_begin) {
+        // Causal mask on tiles reaching past the block's first query.
+        const int my_query = q0[b] + lq;
+        if (t * kKeysPerTile + kKeysPerTile - 1 > q0[b]) {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (t * kKeysPerTile + 32 * kb + 16 * h + 4 * key_grp + r > my_query) s[kb][h][r] = -INFINITY;
+        }
+        // Online softmax with the lazy rescale (bound 2^kRescaleLog2): the first tile of
+        // a block in the wave's range takes the exact max; later tiles use the running
+        // max and check the lane sums, taking the exact max and recomputing only when a
+        // sum exceeds it.
+        auto exact_max_update = [&]() -> bool {
+            float tile_max = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    tile_max = fmaxf(fmaxf(fmaxf(tile_max, s[kb][h][0]), fmaxf(s[kb][h][1], s[kb][h][2])), s[kb][h][3]);
+            tile_max = max_across_groups16(tile_max);
+            const bool grow = tile_max * scale_log2 > m_run[b] * scale_log2 + kRescaleLog2;
+            if (__builtin_amdgcn_ballot_w64(grow) == 0) return false;
+            const float m_new = fmaxf(m_run[b], tile_max);
+            const float alpha = __builtin_amdgcn_exp2f((m_run[b] - m_new) * scale_log2);
+            l_run[b] *= alpha;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) o[b][d] *= alpha;
+            m_run[b] = m_new;
+            return true;
+        };
+        // FP16 P^T operands of the two 32-key blocks and the lane's FP32 sum of the
+        // unrounded probabilities.
+        f16x8 pf[2];
+        auto probs = [&]() -> float {
+            const float m_scaled = m_run[b] * scale_log2;
+            float part[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                float e[2][4];
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        e[h][r] = __builtin_amdgcn_exp2f(fmaf(s[kb][h][r], scale_log2, -m_scaled));
+                const f16x4 lo = __builtin_shufflevector(pack_rn(e[0][0], e[0][1]), pack_rn(e[0][2], e[0][3]), 0, 1, 2, 3);
+                const f16x4 hi = __builtin_shufflevector(pack_rn(e[1][0], e[1][1]), pack_rn(e[1][2], e[1][3]), 0, 1, 2, 3);
+                pf[kb] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                part[kb] = ((e[0][0] + e[0][1]) + (e[0][2] + e[0][3])) + ((e[1][0] + e[1][1]) + (e[1][2] + e[1][3]));
+            }
+            return part[0] + part[1];
+        };
+        if (first) exact_max_update();
+        float tile_sum = probs();
+        if (!first && __builtin_amdgcn_ballot_w64(tile_sum > kTileSumBound) != 0) {
+            if (exact_max_update()) tile_sum = probs();
+        }
+        l_run[b] += tile_sum;
+        // O^T += V^T P^T for the two 32-key blocks and the four 16-dim blocks.
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int dblk = 0; dblk < 4; ++dblk)
+                o[b][dblk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[kb][dblk], pf[kb], o[b][dblk], 0, 0, 0);
+    };
+
+    for (int t = t_begin; t < t_end; ++t) {
+        const int st = (t - t_begin) & 1;
+        if (t + 1 < t_end) {
+            dma_tile(t + 1, st ^ 1);
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerTile) : "memory");  // tile t (and Q) landed
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        const bool first = t == t_begin;
+        const bool both = t < tiles1;
+        if (first) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks)
-                    qf[ks] = *reinterpret_cast<const f16x8*>(my_q + b * kQBlockBytes + q_off[ks]);
-            }
-            const uint8_t* k_lds = my_stages + st * kStageBytes;
-            const uint8_t* v_lds = k_lds + kTileBytes;
-            const int t = b == 0 ? j : j - tiles0;
-
-            f32x4 s[2][2];
-            const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const uint8_t* rows = k_lds + (32 * kb + 16 * h) * kRowBytes;
-                    const f16x8 k0 = *reinterpret_cast<const f16x8*>(rows + k_off[0]);
-                    const f16x8 k1 = *reinterpret_cast<const f16x8*>(rows + k_off[1]);
-                    s[kb][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, qf[0], zero, 0, 0, 0);
-                    s[kb][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qf[1], s[kb][h], 0, 0, 0);
-                }
-            // Causal mask on tiles reaching past the block's first query.
-            const int my_query = q0[b] + lq;
-            if (t * kKeysPerTile + kKeysPerTile - 1 > q0[b]) {
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                    for (int h = 0; h < 2; ++h)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            if (t * kKeysPerTile + 32 * kb + 16 * h + 4 * key_grp + r > my_query) s[kb][h][r] = -INFINITY;
-            }
-
-            // Online softmax with the lazy rescale (bound 2^kRescaleLog2): the first tile of
-            // a segment takes the exact max; later tiles use the running max and check the
-            // lane sums, taking the exact max and recomputing only when a sum exceeds it.
-            auto exact_max_update = [&]() -> bool {
-                float tile_max = -INFINITY;
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                    for (int h = 0; h < 2; ++h)
-                        tile_max = fmaxf(fmaxf(fmaxf(tile_max, s[kb][h][0]), fmaxf(s[kb][h][1], s[kb][h][2])), s[kb][h][3]);
-                tile_max = max_across_groups16(tile_max);
-                const bool grow = tile_max * scale_log2 > m_run[b] * scale_log2 + kRescaleLog2;
-                if (__builtin_amdgcn_ballot_w64(grow) == 0) return false;
-                const float m_new = fmaxf(m_run[b], tile_max);
-                const float alpha = __builtin_amdgcn_exp2f((m_run[b] - m_new) * scale_log2);
-                l_run[b] *= alpha;
-#pragma unroll
-                for (int d = 0; d < 4; ++d) o[b][d] *= alpha;
-                m_run[b] = m_new;
-                return true;
-            };
-            // FP16 P^T operands of the two 32-key blocks and the lane's FP32 sum of the
-            // unrounded probabilities.
-            f16x8 pf[2];
-            auto probs = [&]() -> float {
-                const float m_scaled = m_run[b] * scale_log2;
-                float part[2];
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-                    float e[2][4];
-#pragma unroll
-                    for (int h = 0; h < 2; ++h)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            e[h][r] = __builtin_amdgcn_exp2f(fmaf(s[kb][h][r], scale_log2, -m_scaled));
-                    const f16x4 lo = __builtin_shufflevector(pack_rn(e[0][0], e[0][1]), pack_rn(e[0][2], e[0][3]), 0, 1, 2, 3);
-                    const f16x4 hi = __builtin_shufflevector(pack_rn(e[1][0], e[1][1]), pack_rn(e[1][2], e[1][3]), 0, 1, 2, 3);
-                    pf[kb] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-                    part[kb] = ((e[0][0] + e[0][1]) + (e[0][2] + e[0][3])) + ((e[1][0] + e[1][1]) + (e[1][2] + e[1][3]));
-                }
-                return part[0] + part[1];
-            };
-            const bool first = j == j_begin;
-            if (first) exact_max_update();
-            float tile_sum = probs();
-            if (!first && __builtin_amdgcn_ballot_w64(tile_sum > kTileSumBound) != 0) {
-                if (exact_max_update()) tile_sum = probs();
-            }
-            l_run[b] += tile_sum;
-
-            // O^T += V^T P^T for the two 32-key blocks and the four 16-dim blocks.
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int dblk = 0; dblk < 4; ++dblk) {
-                    const f16x4 lo = lds_read_transposed(v_lds + (32 * kb) * kRowBytes + v_off[dblk]);
-                    const f16x4 hi = lds_read_transposed(v_lds + (32 * kb + 16) * kRowBytes + v_off[dblk]);
-                    const f16x8 vf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-                    o[b][dblk] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[kb], o[b][dblk], 0, 0, 0);
-                }
+                    qf[b][ks] = *reinterpret_cast<const f16x8*>(my_q + b * kQBlockBytes + q_off[ks]);
         }
-    };
-    run_block(std::integral_constant<int, 0>{}, t_begin, min(t_end, tiles0));
-    run_block(std::integral_constant<int, 1>{}, max(t_begin, tiles0), t_end);
+        const uint8_t* k_lds = my_stages + st * kStageBytes;
+        const uint8_t* v_lds = k_lds + kTileBytes;
+        f16x8 kf[2][2][2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint8_t* rows = k_lds + (32 * kb + 16 * h) * kRowBytes;
+                kf[kb][h][0] = *reinterpret_cast<const f16x8*>(rows + k_off[0]);
+                kf[kb][h][1] = *reinterpret_cast<const f16x8*>(rows + k_off[1]);
+            }
+        f16x8 vf[2][4];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int dblk = 0; dblk < 4; ++dblk) {
+                const f16x4 lo = lds_read_transposed(v_lds + (32 * kb) * kRowBytes + v_off[dblk]);
+                const f16x4 hi = lds_read_transposed(v_lds + (32 * kb + 16) * kRowBytes + v_off[dblk]);
+                vf[kb][dblk] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            }
+        block_tile(std::integral_constant<int, 0>{}, t, first, kf, vf);
+        if (both) block_tile(std::integral_constant<int, 1>{}, t, first, kf, vf);
+    }
 
     // Merge the partial results of each block (stages are free once every wave is done;
     // a wave without tiles still has its Q DMA to wait for).

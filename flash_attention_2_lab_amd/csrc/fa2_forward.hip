@@ -2015,7 +2015,7 @@ bool use_128_query_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
 
 constexpr int64_t kSplitWideMaxBlocks = 256;
 constexpr int64_t kEightWaveMinKeys = 2048;
-constexpr int64_t kPairs16MinKeys = 1024;
+constexpr int64_t kPairs16MinKeys = 512;
 constexpr int64_t kDmaWavesMinKeys = 1024;
 
 // The kernel a forward call with these sizes runs (the single place the choice is made).
@@ -2029,11 +2029,11 @@ fa2_forward_kernel choose_kernel(int64_t batch_heads, int64_t seq_len, bool caus
         return FA2_KERNEL_128_QUERY;
     const int64_t query_blocks = (seq_len + kQueriesPerWave - 1) / kQueriesPerWave;
     if (batch_heads * query_blocks > kSplitWideMaxBlocks) return FA2_KERNEL_KEY_SPLIT_32;
-    // Causal, one workgroup per CU, from 1024 to 2047 keys: pairs of 16-query blocks, so
+    // Causal, one workgroup per CU, from 512 to 2047 keys: pairs of 16-query blocks, so
     // every workgroup has the same key tiles instead of the last block having all of
-    // them. Measured on MI355X against 32-query blocks: -16% at B1 H4 N1920, even at
-    // B1 H8 N1024 (where each CU streams a whole head's K/V either way, and that
-    // fetch, not the compute, sets the time) and 4-6% slower at 128-512 keys.
+    // them. Measured on MI355X against 32-query blocks: -13% at B1 H8 N896, -7% at
+    // B1 H8 N768, -2% at N512 (-6.5% at B1 H8 N1024 and -16% at B1 H4 N1920 before the
+    // light block shared the heavy block's key tiles); 3-7% slower at 128-256 keys.
     if (causal && seq_len % 64 == 0 && seq_len >= kPairs16MinKeys && seq_len < kEightWaveMinKeys)
         return FA2_KERNEL_KEY_SPLIT_PAIRS16;
     // One workgroup per CU: from 2048 keys on, 8 waves with two 32-key stages each

@@ -67,7 +67,9 @@ K = capi
     (1, 410, 1280, True, K.FA2_KERNEL_256_QUERY), (1, 409, 1280, True, K.FA2_KERNEL_128_QUERY),
     (1, 64, 1024, True, K.FA2_KERNEL_128_QUERY), (1, 63, 1024, True, K.FA2_KERNEL_KEY_SPLIT_32),
     (1, 8, 1024, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16), (1, 2, 128, True, K.FA2_KERNEL_KEY_SPLIT_64),
-    (1, 8, 896, True, K.FA2_KERNEL_KEY_SPLIT_64), (1, 2, 1024, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16),
+    (1, 8, 896, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16), (1, 2, 1024, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16),
+    (1, 8, 512, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16), (1, 8, 384, True, K.FA2_KERNEL_KEY_SPLIT_64),
+    (1, 8, 544, True, K.FA2_KERNEL_KEY_SPLIT_64),
     (1, 4, 1920, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16), (1, 4, 1040, True, K.FA2_KERNEL_KEY_SPLIT_64),
     # Key-split shapes from 2048 keys on split each block's keys over 8 waves.
     (1, 2, 4096, False, K.FA2_KERNEL_KEY_SPLIT_8_WAVES), (1, 1, 2048, True, K.FA2_KERNEL_KEY_SPLIT_8_WAVES),

@@ -48,7 +48,9 @@ CASES = [
     (1, 8, 1024, True, "key-split, pairs of 16-query blocks (256 pairs)", K.FA2_KERNEL_KEY_SPLIT_PAIRS16),
     (1, 4, 1920, True, "key-split, pairs of 16-query blocks (the longest below 2048 keys)",
      K.FA2_KERNEL_KEY_SPLIT_PAIRS16),
-    (1, 8, 896, True, "key-split, 64-key tiles (224 blocks below 1024 keys)", K.FA2_KERNEL_KEY_SPLIT_64),
+    (1, 8, 896, True, "key-split, pairs of 16-query blocks (896 keys)", K.FA2_KERNEL_KEY_SPLIT_PAIRS16),
+    (1, 8, 512, True, "key-split, pairs of 16-query blocks (the shortest, 512 keys)", K.FA2_KERNEL_KEY_SPLIT_PAIRS16),
+    (1, 8, 384, True, "key-split, 64-key tiles (below 512 keys)", K.FA2_KERNEL_KEY_SPLIT_64),
     (1, 2, 1024, True, "key-split, pairs of 16-query blocks (64 pairs)", K.FA2_KERNEL_KEY_SPLIT_PAIRS16),
     (3, 3, 1024, True, "key-split, 32-key tiles (288 query blocks)", K.FA2_KERNEL_KEY_SPLIT_32),
     (1, 4, 1024, False, "key-split, 64-key tiles, DMA waves (1024 keys)", K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES),

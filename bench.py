@@ -11,8 +11,10 @@ mirrored order - K/2 noncausal, K/2 causal, the other K/2 causal, the other K/2
 noncausal (the same work as K interleaved steps, with neither mode always first) -
 with HIP events on the launch stream between the batches: the reference harness's
 method (benchmarks/harness.py:34-71: events around back-to-back calls). Those events
-give each kernel's average launch duration for the `roofline` object; wall-clock time
-between two device synchronisations gives `ms_per_step`.
+give each kernel's average launch duration for the `roofline` object (the region's
+first call, which the device starts from idle, is left out of that average);
+wall-clock time between two device synchronisations, over all K steps, gives
+`ms_per_step`.
 
 Also reported (extra keys, each timed the same way after the main region):
 `north_star` - B16 H16 N4096 noncausal and causal (the >=50%-of-MFMA-peak target)
@@ -70,7 +72,13 @@ def time_kernel_batches(entry, inputs, modes, steps, warmup):
     events on the current stream. With two modes the calls run as four back-to-back
     batches in mirrored order - first half of mode A, first half of mode B, second
     half of B, second half of A - so neither mode is always the one timed right after
-    the warmup. Returns (wall_s, {mode: avg_s})."""
+    the warmup. Returns (wall_s, {mode: avg_s}).
+
+    The wall clock covers all `steps` calls per mode. The per-call averages leave out
+    the region's first call: after the opening synchronisation the device waits idle
+    for the host to launch it, and that wait is not the kernel's duration. An event
+    recorded right after that call is reached when it completes, and from there on the
+    host launches ahead of the device, so the events time back-to-back kernels."""
     import torch
 
     q, k, v = inputs
@@ -80,22 +88,29 @@ def time_kernel_batches(entry, inputs, modes, steps, warmup):
     first = steps // 2
     halves = [(causal, first) for causal in modes] + [(causal, steps - first) for causal in reversed(modes)]
     halves = [(causal, n) for causal, n in halves if n > 0]
+    skip_first = steps > 1  # the first mode keeps at least one timed call
     stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
     events = [torch.cuda.Event(enable_timing=True) for _ in range(len(halves) + 1)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    events[0].record(stream)
+    start.record(stream)
     for i, (causal, n) in enumerate(halves):
-        for _ in range(n):
+        for j in range(n):
             entry(q, k, v, causal)
+            if i == 0 and j == 0:
+                events[0].record(stream)
         events[i + 1].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per_kernel = {}
+    per_kernel, calls = {}, {}
     for i, (causal, n) in enumerate(halves):
         mode = "causal" if causal else "noncausal"
-        per_kernel[mode] = per_kernel.get(mode, 0.0) + events[i].elapsed_time(events[i + 1]) / 1e3
-    return wall, {mode: total / steps for mode, total in per_kernel.items()}
+        begin = events[i] if i > 0 or skip_first else start
+        timed = n - 1 if i == 0 and skip_first else n
+        per_kernel[mode] = per_kernel.get(mode, 0.0) + begin.elapsed_time(events[i + 1]) / 1e3
+        calls[mode] = calls.get(mode, 0) + timed
+    return wall, {mode: total / calls[mode] for mode, total in per_kernel.items()}
 
 
 def time_in_graph(entry, inputs, modes, steps, replays=3):

@@ -7,14 +7,18 @@ least 8 tiles or the grid 2048; else pairs of query tiles when a head has an eve
 number of them, one tile per workgroup from 2048 when odd), the
 128-query kernel from 256 (noncausal) or 512 (causal) groups of 128 queries, and
 otherwise the key-split kernel: up to 256 query blocks of 32, 4 waves with 64-key tiles
-(8 waves with 32-key tiles from 2048 keys on; causal from 1024 to 2047 keys, pairs of
-16-query blocks), and 32-key tiles beyond. Each case below sits one step below or at a threshold, and
-`fa2_forward_plan` (the function the forward dispatches through) must name the kernel
-the case is meant to reach; every row of the first and last head and sampled rows of
-the others are checked against the FP32 oracle (atol 2e-3 + rtol 1e-2).
+(noncausal from 1024 keys with dedicated DMA waves; causal from 512 to 2047 keys, pairs
+of 16-query blocks; 8 waves with 32-key tiles from 2048 keys on), and 32-key tiles
+beyond. Each case below sits one step below or at a threshold, and `fa2_forward_plan`
+(the function the forward dispatches through) must name the kernel the case is meant
+to reach; every row of the first and last head and sampled rows of the others are
+checked against the FP32 oracle (atol 2e-3 + rtol 1e-2). A second set of shapes, drawn
+from a seeded generator over the whole routing table, is checked the same way.
 """
 
 from __future__ import annotations
+
+import math
 
 import pytest
 import torch
@@ -66,22 +70,49 @@ CASES = [
 ]
 
 
+KERNEL_IDS = (K.FA2_KERNEL_128_QUERY, K.FA2_KERNEL_256_QUERY, K.FA2_KERNEL_256_QUERY_PAIRS,
+              K.FA2_KERNEL_KEY_SPLIT_64, K.FA2_KERNEL_KEY_SPLIT_32, K.FA2_KERNEL_KEY_SPLIT_8_WAVES,
+              K.FA2_KERNEL_KEY_SPLIT_PAIRS16, K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES)
+
+
+def _random_shapes(per_kernel, seed):
+    # (batch, heads, seq_len, causal) drawn from one seeded stream: seq_len a multiple of
+    # 128 up to 4096, batch*heads log-uniform from 1 to 576, at most 576 heads of 1024
+    # keys' worth of work. The first `per_kernel` draws that each kernel runs are kept,
+    # so every kernel of the routing table is checked on shapes nobody picked by hand.
+    gen = torch.Generator().manual_seed(seed)
+    picked = {kernel: [] for kernel in KERNEL_IDS}
+    for _ in range(20000):
+        if all(len(v) == per_kernel for v in picked.values()):
+            break
+        seq_len = 128 * int(torch.randint(1, 33, (1,), generator=gen))
+        batch = int(torch.randint(1, 5, (1,), generator=gen))
+        heads = max(1, round(math.exp(float(torch.rand(1, generator=gen)) * math.log(576 / batch))))
+        causal = bool(torch.randint(0, 2, (1,), generator=gen))
+        if batch * heads * seq_len > 576 * 1024:
+            continue
+        kernel = capi.forward_plan(batch, heads, seq_len, causal)
+        if len(picked[kernel]) < per_kernel:
+            picked[kernel].append((batch, heads, seq_len, causal))
+    return [shape for kernel in KERNEL_IDS for shape in picked[kernel]]
+
+
+RANDOM_SHAPES = _random_shapes(4, seed=2024)
+
+
 def _inputs(batch, heads, seq_len, seed):
     gen = torch.Generator().manual_seed(seed)
     shape = (batch, heads, seq_len, 64)
     return tuple(torch.randn(shape, generator=gen).half() for _ in range(3))
 
 
-@pytest.mark.parametrize("batch, heads, seq_len, causal, kernel, kernel_id", CASES,
-                         ids=[("causal: " if c[3] else "noncausal: ") + c[4] for c in CASES])
-def test_threshold_shapes_match_oracle(batch, heads, seq_len, causal, kernel, kernel_id):
-    assert capi.forward_plan(batch, heads, seq_len, causal) == kernel_id
-    q, k, v = _inputs(batch, heads, seq_len, seed=31)
+def _check_against_oracle(batch, heads, seq_len, causal, seed):
+    q, k, v = _inputs(batch, heads, seq_len, seed=seed)
     out = ENTRY(q.cuda(), k.cuda(), v.cuda(), causal)
     torch.cuda.synchronize()
     out = out.cpu()
     assert torch.isfinite(out).all()
-    gen = torch.Generator().manual_seed(32)
+    gen = torch.Generator().manual_seed(seed + 1)
     rows = [(0, 0, i) for i in range(seq_len)] + [(batch - 1, heads - 1, i) for i in range(seq_len)]
     rows += [(int(torch.randint(batch, (1,), generator=gen)), int(torch.randint(heads, (1,), generator=gen)),
               int(torch.randint(seq_len, (1,), generator=gen))) for _ in range(96)]
@@ -89,3 +120,16 @@ def test_threshold_shapes_match_oracle(batch, heads, seq_len, causal, kernel, ke
     expected = attention_rows_fp32(q, k, v, rows, causal=causal)
     actual = torch.stack([out[b, h, i] for b, h, i in rows]).float()
     torch.testing.assert_close(actual, expected, atol=2e-3, rtol=1e-2)
+
+
+@pytest.mark.parametrize("batch, heads, seq_len, causal, kernel, kernel_id", CASES,
+                         ids=[("causal: " if c[3] else "noncausal: ") + c[4] for c in CASES])
+def test_threshold_shapes_match_oracle(batch, heads, seq_len, causal, kernel, kernel_id):
+    assert capi.forward_plan(batch, heads, seq_len, causal) == kernel_id
+    _check_against_oracle(batch, heads, seq_len, causal, seed=31)
+
+
+@pytest.mark.parametrize("batch, heads, seq_len, causal", RANDOM_SHAPES,
+                         ids=[f"B{b}H{h}N{n}{'c' if c else 'nc'}" for b, h, n, c in RANDOM_SHAPES])
+def test_random_shapes_match_oracle(batch, heads, seq_len, causal):
+    _check_against_oracle(batch, heads, seq_len, causal, seed=41)

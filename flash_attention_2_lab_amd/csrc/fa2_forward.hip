@@ -149,6 +149,49 @@ __device__ __forceinline__ void wait_dma_and_barrier() {
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kPending) : "memory");
 }
 
+// Causal head groups: with every XCD owning batch_heads / 8 whole heads, the XCD
+// runs them a group at a time, and within a group the query tiles (or blocks) run
+// heaviest first across all its heads: every head's last tile, then every head's
+// second-to-last, and so on. A group has about as many tiles as an XCD has workgroup
+// slots (32 CUs, two workgroups each), so its workgroups start on the same keys
+// together and share its heads' K/V through L2, and the longest-first order drains
+// the slots evenly: heads per group for T tiles per head is 64 / T, from 1 to 8.
+// Head-major order (each head's tiles heaviest first, one head after another) instead
+// starts the heavy tiles of an XCD's later heads only after light ones finish.
+__device__ __forceinline__ uint32_t group_heads(uint32_t tiles_per_head) {
+    return tiles_per_head >= 64 ? 1u : tiles_per_head >= 32 ? 2u : tiles_per_head >= 16 ? 4u : 8u;
+}
+
+// Workgroup -> (batch*head, work item) for grids of `tiles_per_head` items per head.
+// Dispatch is round-robin over the 8 XCDs (id % 8), so every XCD gets a contiguous
+// range of logical items and the items of one head share that XCD's L2. Causal items
+// run in head groups when batch_heads is a multiple of 8, else head by head; `item`
+// counts from the heaviest (item 0 = the last query tile of a head).
+struct WorkItem {
+    uint32_t bh, item;
+};
+template <bool kCausal>
+__device__ __forceinline__ WorkItem xcd_work_item(uint32_t tiles_per_head) {
+    const uint32_t groups = gridDim.x;
+    const uint32_t xcd = blockIdx.x & 7u;
+    const uint32_t slot = blockIdx.x >> 3;
+    const uint32_t per_xcd = groups >> 3;
+    const uint32_t extra = groups & 7u;
+    const uint32_t batch_heads = groups / tiles_per_head;
+    if (kCausal && (batch_heads & 7u) == 0) {
+        const uint32_t xcd_heads = batch_heads >> 3;
+        const uint32_t per_group = group_heads(tiles_per_head);
+        const uint32_t group = slot / (per_group * tiles_per_head);
+        const uint32_t in_group = slot - group * (per_group * tiles_per_head);
+        const uint32_t heads = min(per_group, xcd_heads - group * per_group);  // the last group may be short
+        const uint32_t item = in_group / heads;
+        return {xcd * xcd_heads + group * per_group + (in_group - item * heads), item};
+    }
+    const uint32_t logical = xcd * per_xcd + min(xcd, extra) + slot;
+    const uint32_t bh = logical / tiles_per_head;
+    return {bh, logical - bh * tiles_per_head};
+}
+
 template <bool kCausal, int kWaves>
 __global__ __launch_bounds__(kWaves * 64)
 __attribute__((amdgpu_waves_per_eu(kWaves == 4 ? 2 : 1)))  // 4-wave groups: two waves per SIMD
@@ -180,18 +223,13 @@ void fa2_forward_d64_kernel(const _Float16* __restrict__ query,
     const int lq = lane & 31;   // query column owned by this lane
     const int half = lane >> 5; // which 16 of each 32 keys this lane holds
 
-    // Workgroup -> (batch*head, query tile). Dispatch is round-robin over 8 XCDs
-    // (id % 8); give every XCD a contiguous range of logical tiles so the query
-    // tiles of one head share that XCD's L2.
-    const uint32_t groups = gridDim.x;
-    const uint32_t xcd = blockIdx.x & 7u;
-    const uint32_t slot = blockIdx.x >> 3;
-    const uint32_t per_xcd = groups >> 3;
-    const uint32_t extra = groups & 7u;
-    const uint32_t logical = xcd * per_xcd + min(xcd, extra) + slot;
-    const uint32_t bh = logical / (uint32_t)num_query_tiles;
-    uint32_t qtile = logical - bh * (uint32_t)num_query_tiles;
-    if (kCausal) qtile = (uint32_t)num_query_tiles - 1u - qtile;  // heaviest tiles first
+    // Workgroup -> (batch*head, query tile): XCD-contiguous, causal tiles heaviest
+    // first in head groups. Measured on MI355X against head-major order (same process,
+    // bit-identical): -17% at B1 H32 N4096, -23% at B4 H16 N2048 and B8 H16 N1024, -15%
+    // at B16 H16 N512, -11% at B1 H16 N4096; unchanged with one head per XCD.
+    const WorkItem work = xcd_work_item<kCausal>((uint32_t)num_query_tiles);
+    const uint32_t bh = work.bh;
+    const uint32_t qtile = kCausal ? (uint32_t)num_query_tiles - 1u - work.item : work.item;
 
     const size_t head_offset = (size_t)bh * (size_t)seq_len * kHeadDim;
     const _Float16* __restrict__ q_head = query + head_offset;
@@ -626,17 +664,13 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_splitk_kernel(const _
     const int lq = lane & 31;
     const int half = lane >> 5;
 
-    // Workgroup -> (batch*head, query block), XCD-contiguous; causal blocks run
-    // heaviest first.
-    const uint32_t groups = gridDim.x;
-    const uint32_t xcd = blockIdx.x & 7u;
-    const uint32_t slot = blockIdx.x >> 3;
-    const uint32_t per_xcd = groups >> 3;
-    const uint32_t extra = groups & 7u;
-    const uint32_t logical = xcd * per_xcd + min(xcd, extra) + slot;
-    const uint32_t bh = logical / (uint32_t)num_query_blocks;
-    uint32_t qblock = logical - bh * (uint32_t)num_query_blocks;
-    if (kCausal) qblock = (uint32_t)num_query_blocks - 1u - qblock;
+    // Workgroup -> (batch*head, query block): XCD-contiguous, head by head, causal
+    // blocks heaviest first. (Head groups, as in the 128-query kernel, measured -1% to
+    // -3% at B1 H32 N1024 and B4 H8 N1024 but +6% to +10% at B1 H40 N1024 and B1 H24
+    // N1024: these grids are at most a few rounds of short workgroups.)
+    const WorkItem work = xcd_work_item<false>((uint32_t)num_query_blocks);
+    const uint32_t bh = work.bh;
+    const uint32_t qblock = kCausal ? (uint32_t)num_query_blocks - 1u - work.item : work.item;
 
     const size_t head_offset = (size_t)bh * (size_t)seq_len * kHeadDim;
     const _Float16* __restrict__ q_head = query + head_offset;
@@ -1565,14 +1599,11 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_pairs16_kernel(const 
 //    so every workgroup streams the same 4(T+1) key tiles: better when the grid is
 //    only one or two rounds of workgroups, where the group order has too few tiles
 //    to balance; the light pass re-reads keys that have left L2.
-// Heads per group for T query tiles per head: 64 / T, from 1 to 8. Measured on
+// Heads per group for T query tiles per head (group_heads): 64 / T, from 1 to 8. Measured on
 // MI355X (same process): at T = 16 (B16 H16 N4096) groups of 4 run 2.6% faster than
 // groups of 8 and fetch 1.04x Q+K+V from HBM against 1.69x; at T = 64 (B2 H32 N16384)
 // one head per group fetches 1.13x against 6.9x for 8, within 1.3% of the fastest
 // group size.
-__device__ __forceinline__ uint32_t group_heads(uint32_t tiles_per_head) {
-    return tiles_per_head >= 64 ? 1u : tiles_per_head >= 32 ? 2u : tiles_per_head >= 16 ? 4u : 8u;
-}
 
 template <bool kCausal, bool kPairs>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
@@ -1595,36 +1626,14 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
     const int lq = lane & 31;
     const int half = lane >> 5;
 
-    // Workgroup -> (batch*head, work item), XCD-contiguous: dispatch is round-robin
-    // over the 8 XCDs (id % 8), so every XCD gets a contiguous range of logical items.
-    // Noncausal: an item is one query tile. Causal: see the schedules above; `item`
-    // counts from the heaviest tile (item 0 = tile T-1).
+    // Workgroup -> (batch*head, work item), XCD-contiguous. Noncausal: an item is one
+    // query tile. Causal: see the schedules above (head groups, or pairs head by head);
+    // `item` counts from the heaviest tile (item 0 = tile T-1).
     static_assert(kCausal || !kPairs, "pairs are a causal schedule");
-    const uint32_t groups = gridDim.x;
-    const uint32_t xcd = blockIdx.x & 7u;
-    const uint32_t slot = blockIdx.x >> 3;
-    const uint32_t per_xcd = groups >> 3;
-    const uint32_t extra = groups & 7u;
-    const uint32_t logical = xcd * per_xcd + min(xcd, extra) + slot;
     const uint32_t tiles_per_head = (uint32_t)num_query_tiles;
-    const uint32_t batch_heads = kPairs ? groups * 2u / tiles_per_head : groups / tiles_per_head;
-    uint32_t bh, item;
-    if (kCausal && !kPairs && (batch_heads & 7u) == 0) {
-        // Every XCD owns batch_heads / 8 whole heads (slots 0.. of its dispatch order)
-        // and runs them a group at a time, heaviest tiles of the group first.
-        const uint32_t xcd_heads = batch_heads >> 3;
-        const uint32_t per_group = group_heads(tiles_per_head);
-        const uint32_t group = slot / (per_group * tiles_per_head);
-        const uint32_t in_group = slot - group * (per_group * tiles_per_head);
-        const uint32_t heads = min(per_group, xcd_heads - group * per_group);  // the last group may be short
-        item = in_group / heads;
-        bh = xcd * xcd_heads + group * per_group + (in_group - item * heads);
-    } else {
-        // Head-major; a causal head's tiles heaviest first (or its pairs).
-        const uint32_t items = kPairs ? tiles_per_head / 2u : tiles_per_head;
-        bh = logical / items;
-        item = logical - bh * items;
-    }
+    const WorkItem work = xcd_work_item<kCausal && !kPairs>(kPairs ? tiles_per_head / 2u : tiles_per_head);
+    const uint32_t bh = work.bh;
+    const uint32_t item = work.item;
     constexpr int passes = kPairs ? 2 : 1;
 
     // Q and O of the head through buffer descriptors (SGPR base, 32-bit lane offsets):

@@ -2070,11 +2070,33 @@ bool use_head_groups(int64_t batch_heads, int64_t tiles_per_head) {
 // slower (B1 H32 N4096, B1 H8 N16384). Causal problems with an odd number of tiles
 // per head run one tile per workgroup, and only from 2048 workgroups, where that
 // schedule was measured no slower than the 128-query kernel.
+//
+// Noncausal grids that end in a partial round: both kernels run two workgroups per
+// CU (512 slots), and a last round of at most 256 workgroups runs them one per CU,
+// each faster than when it shares its CU but with the chip half empty. Time model in
+// rounds of the wide kernel: `full` rounds of 1, a last round of 1 when more than half
+// full, else 0.645 (wide) or 0.58 (128-query: 1.29x and 1.72x a shared workgroup's
+// rate alone on a CU, measured with LDS padding); the 128-query kernel's rounds cost
+// 0.5375 (half the work, 7.5% slower per FLOP). It runs the grid when its modeled time
+// is more than 5% shorter. Measured on MI355X (same process, wide -> 128-query): -15%
+// at 576 wide workgroups (B9 H8 N2048, B1 H36 N4096), -13% at 640 (B5 H16 N2048,
+// B1 H40 N4096), -4% at 768, +1% at 896, +2.4% at 1280, +7.5% at 1536 and 4096.
+double modeled_rounds(int64_t workgroups, double lone_round) {
+    const int64_t full = workgroups / 512;
+    const int64_t rest = workgroups % 512;
+    return (double)full + (rest == 0 ? 0.0 : rest <= 256 ? lone_round : 1.0);
+}
+
 bool use_wide_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
     if (seq_len % 256 != 0) return false;
     const int64_t tiles = seq_len / 256;
     if (causal && tiles % 2 != 0) return batch_heads * tiles >= 2048;
-    return batch_heads * (causal ? tiles / 2 : tiles) >= 512;
+    const int64_t workgroups = batch_heads * (causal ? tiles / 2 : tiles);
+    if (workgroups < 512) return false;
+    if (causal) return true;
+    const double wide = modeled_rounds(workgroups, 0.645);
+    const double narrow = 0.5375 * modeled_rounds(2 * workgroups, 0.58);
+    return !(narrow < 0.95 * wide);
 }
 
 // 128-query workgroups (4 waves) when they fill the chip (two per CU); otherwise

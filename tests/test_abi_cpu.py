@@ -55,6 +55,11 @@ K = capi
     (16, 16, 4096, False, K.FA2_KERNEL_256_QUERY), (1, 32, 1024, False, K.FA2_KERNEL_128_QUERY),
     (1, 31, 1024, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 8, 1024, False, K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES),
     (1, 9, 1024, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 8, 128, False, K.FA2_KERNEL_KEY_SPLIT_64),
+    # ... except where the 256-query grid ends in a last round at most half full and
+    # the 128-query kernel's finer rounds are modeled more than 5% faster.
+    (1, 36, 4096, False, K.FA2_KERNEL_128_QUERY), (5, 16, 2048, False, K.FA2_KERNEL_128_QUERY),
+    (9, 16, 2048, False, K.FA2_KERNEL_128_QUERY), (3, 16, 4096, False, K.FA2_KERNEL_256_QUERY),
+    (7, 16, 2048, False, K.FA2_KERNEL_256_QUERY), (6, 16, 4096, False, K.FA2_KERNEL_256_QUERY),
     # Causal: 256-query from 512 workgroups of tile pairs when a head has an even
     # number T of tiles, single tiles from 2048 with an odd number. Single tiles in
     # head groups (batch*heads a multiple of 8) from T >= 8 or 2048 tiles; pairs below

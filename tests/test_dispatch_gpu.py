@@ -1,7 +1,8 @@
 """GPU parity on both sides of every kernel-choice threshold of the forward.
 
 The forward picks its kernel from (batch*heads, seq_len, causal) (fa2_forward.hip,
-`choose_kernel`): the 256-query kernel from 512 workgroups (causal: one query tile per
+`choose_kernel`): the 256-query kernel from 512 workgroups (noncausal: unless its grid
+ends in a partial round that the 128-query kernel's finer rounds finish sooner; causal: one query tile per
 workgroup in per-XCD head groups when batch*heads is a multiple of 8 and a head has at
 least 8 tiles or the grid 2048; else pairs of query tiles when a head has an even
 number of them, one tile per workgroup from 2048 when odd), the
@@ -36,6 +37,8 @@ CASES = [
     # (batch, heads, seq_len, causal, kernel it runs, FA2_KERNEL_* id)
     (1, 127, 1024, False, "128-query (508 groups of 256)", K.FA2_KERNEL_128_QUERY),
     (1, 128, 1024, False, "256-query (512 groups of 256)", K.FA2_KERNEL_256_QUERY),
+    (1, 36, 4096, False, "128-query (576 wide workgroups: a partial last round)", K.FA2_KERNEL_128_QUERY),
+    (3, 16, 4096, False, "256-query (768 wide workgroups: a half-full last round)", K.FA2_KERNEL_256_QUERY),
     (1, 31, 1024, False, "key-split, 32-key tiles (248 groups of 128)", K.FA2_KERNEL_KEY_SPLIT_32),
     (1, 32, 1024, False, "128-query (256 groups of 128)", K.FA2_KERNEL_128_QUERY),
     (1, 8, 1024, False, "key-split, 64-key tiles, DMA waves (256 query blocks)", K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES),

@@ -2102,14 +2102,20 @@ bool use_wide_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
 // 128-query workgroups (4 waves) when they fill the chip (two per CU); otherwise
 // the key-split kernel (one 32-query block per workgroup, keys split over 4 waves).
 // Kernel choice from measured crossovers on MI355X (B*H*N/128 = number of
-// 128-query groups): the 128-query kernel once there are at least two groups per CU
-// for causal problems (fewer leave CUs idle behind the longest causal groups) and
-// one per CU for noncausal ones; below that the key-split kernel, with 64-key tiles
-// while one workgroup per CU covers the grid (256 or fewer 32-query blocks) and
-// 32-key tiles (half the LDS, two workgroups per CU) beyond.
+// 128-query groups): noncausal from one group per CU. Causal problems need more,
+// since fewer groups leave CUs idle behind the longest causal groups: from 320
+// groups when batch*heads is a multiple of 8 (the causal head groups balance the
+// XCDs' slots), from 448 otherwise. Measured against the key-split kernel (same
+// process): -7% to -22% at 320-448 groups (B1 H40 N1024, B1 H24 N2048, B1 H48 N1024,
+// B1 H96 N512, B1 H56 N1024; B1 H28 N2048 -9%), +5% to +37% at 256-288 groups and at
+// 320-384 groups without head groups (B1 H8 N4096, B1 H16 N2048, B1 H72 N512, B1 H20
+// N2048, B1 H12 N4096). Below that the key-split kernel, with 64-key tiles while one
+// workgroup per CU covers the grid (256 or fewer 32-query blocks) and 32-key tiles
+// (half the LDS, two workgroups per CU) beyond.
 bool use_128_query_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
     const int64_t groups = batch_heads * (seq_len / 128);
-    return groups >= (causal ? 512 : 256);
+    if (!causal) return groups >= 256;
+    return groups >= (batch_heads % 8 == 0 ? 320 : 448);
 }
 
 constexpr int64_t kSplitWideMaxBlocks = 256;

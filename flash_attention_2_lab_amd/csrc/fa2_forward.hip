@@ -164,32 +164,57 @@ __device__ __forceinline__ uint32_t group_heads(uint32_t tiles_per_head) {
 
 // Workgroup -> (batch*head, work item) for grids of `tiles_per_head` items per head.
 // Dispatch is round-robin over the 8 XCDs (id % 8), so every XCD gets a contiguous
-// range of logical items and the items of one head share that XCD's L2. Causal items
-// run in head groups when batch_heads is a multiple of 8, else head by head; `item`
-// counts from the heaviest (item 0 = the last query tile of a head).
+// range of logical (head-major) items and the items of one head share that XCD's L2.
+// `item` counts from the heaviest (item 0 = the last query tile of a head).
+// Noncausal: the XCD's range in order. Causal: the range in chunks of group_heads(T)
+// heads' worth of items, each chunk in level order (every head's item 0, then every
+// head's item 1, ...). When batch_heads is a multiple of 8 the chunks are whole heads:
+// the head groups above. Otherwise the XCD ranges split heads, and a chunk's first and
+// last head may contribute only some levels; a binary search over the levels finds the
+// slot's level from the count of the chunk's items below each level.
 struct WorkItem {
     uint32_t bh, item;
 };
 template <bool kCausal>
 __device__ __forceinline__ WorkItem xcd_work_item(uint32_t tiles_per_head) {
+    const uint32_t T = tiles_per_head;
     const uint32_t groups = gridDim.x;
     const uint32_t xcd = blockIdx.x & 7u;
     const uint32_t slot = blockIdx.x >> 3;
     const uint32_t per_xcd = groups >> 3;
     const uint32_t extra = groups & 7u;
-    const uint32_t batch_heads = groups / tiles_per_head;
-    if (kCausal && (batch_heads & 7u) == 0) {
-        const uint32_t xcd_heads = batch_heads >> 3;
-        const uint32_t per_group = group_heads(tiles_per_head);
-        const uint32_t group = slot / (per_group * tiles_per_head);
-        const uint32_t in_group = slot - group * (per_group * tiles_per_head);
-        const uint32_t heads = min(per_group, xcd_heads - group * per_group);  // the last group may be short
-        const uint32_t item = in_group / heads;
-        return {xcd * xcd_heads + group * per_group + (in_group - item * heads), item};
+    const uint32_t xcd_begin = xcd * per_xcd + min(xcd, extra);
+    if (!kCausal) {
+        const uint32_t logical = xcd_begin + slot;
+        const uint32_t bh = logical / T;
+        return {bh, logical - bh * T};
     }
-    const uint32_t logical = xcd * per_xcd + min(xcd, extra) + slot;
-    const uint32_t bh = logical / tiles_per_head;
-    return {bh, logical - bh * tiles_per_head};
+    const uint32_t xcd_end = xcd_begin + per_xcd + (xcd < extra ? 1u : 0u);
+    const uint32_t chunk_items = group_heads(T) * T;
+    const uint32_t chunk = slot / chunk_items;
+    const uint32_t begin = xcd_begin + chunk * chunk_items;
+    const uint32_t end = min(begin + chunk_items, xcd_end);  // exclusive; the last chunk may be short
+    const uint32_t rank = slot - chunk * chunk_items;        // position in level order
+    const uint32_t head_first = begin / T, level_first = begin - head_first * T;  // its levels >= level_first
+    const uint32_t head_last = (end - 1) / T, level_last = (end - 1) - head_last * T;  // its levels <= level_last
+    // Items of the chunk on levels below k.
+    auto below = [&](uint32_t k) -> uint32_t {
+        if (head_first == head_last) return k <= level_first ? 0u : min(k, level_last + 1u) - level_first;
+        const uint32_t full_heads = head_last - head_first - 1u;
+        return full_heads * k + (k > level_first ? k - level_first : 0u) + min(k, level_last + 1u);
+    };
+    uint32_t lo = 0, hi = T;  // below(lo) <= rank < below(hi)
+    while (hi - lo > 1u) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (below(mid) <= rank) lo = mid;
+        else hi = mid;
+    }
+    const uint32_t r = rank - below(lo);  // among the heads that have level lo, in head order
+    uint32_t bh;
+    if (head_first == head_last) bh = head_first;
+    else if (lo >= level_first) bh = head_first + r;  // the first head has this level
+    else bh = head_first + 1u + r;
+    return {bh, lo};
 }
 
 template <bool kCausal, int kWaves>
@@ -2102,20 +2127,18 @@ bool use_wide_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
 // 128-query workgroups (4 waves) when they fill the chip (two per CU); otherwise
 // the key-split kernel (one 32-query block per workgroup, keys split over 4 waves).
 // Kernel choice from measured crossovers on MI355X (B*H*N/128 = number of
-// 128-query groups): noncausal from one group per CU. Causal problems need more,
-// since fewer groups leave CUs idle behind the longest causal groups: from 320
-// groups when batch*heads is a multiple of 8 (the causal head groups balance the
-// XCDs' slots), from 448 otherwise. Measured against the key-split kernel (same
-// process): -7% to -22% at 320-448 groups (B1 H40 N1024, B1 H24 N2048, B1 H48 N1024,
-// B1 H96 N512, B1 H56 N1024; B1 H28 N2048 -9%), +5% to +37% at 256-288 groups and at
-// 320-384 groups without head groups (B1 H8 N4096, B1 H16 N2048, B1 H72 N512, B1 H20
-// N2048, B1 H12 N4096). Below that the key-split kernel, with 64-key tiles while one
-// workgroup per CU covers the grid (256 or fewer 32-query blocks) and 32-key tiles
-// (half the LDS, two workgroups per CU) beyond.
+// 128-query groups): noncausal from one group per CU, causal from 320 groups (fewer
+// leave CUs idle behind the longest causal groups). Measured against the key-split
+// kernel with the causal tiles in level-ordered chunks (same process): -2% to -23% at
+// 320-504 groups (B1 H40 N1024, B1 H24 N2048, B1 H48 N1024, B1 H56 N1024, B1 H63
+// N1024; B1 H20 N2048, B1 H10 N4096, B1 H12 N4096, B1 H44 N1024, B1 H52 N1024, B1 H28
+// N1536), +5% to +37% at 256-288 groups (B1 H8 N4096, B1 H16 N2048, B4 H8 N1024,
+// B1 H32 N1024, B1 H72 N512). Below that the key-split kernel, with 64-key tiles
+// while one workgroup per CU covers the grid (256 or fewer 32-query blocks) and
+// 32-key tiles (half the LDS, two workgroups per CU) beyond.
 bool use_128_query_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
     const int64_t groups = batch_heads * (seq_len / 128);
-    if (!causal) return groups >= 256;
-    return groups >= (batch_heads % 8 == 0 ? 320 : 448);
+    return groups >= (causal ? 320 : 256);
 }
 
 constexpr int64_t kSplitWideMaxBlocks = 256;

@@ -71,11 +71,11 @@ K = capi
     (1, 66, 4096, True, K.FA2_KERNEL_256_QUERY_PAIRS), (1, 510, 1024, True, K.FA2_KERNEL_256_QUERY_PAIRS),
     (1, 410, 1280, True, K.FA2_KERNEL_256_QUERY), (1, 409, 1280, True, K.FA2_KERNEL_128_QUERY),
     (1, 64, 1024, True, K.FA2_KERNEL_128_QUERY),
-    # 128-query from 320 groups of 128 with head groups (batch*heads % 8 == 0), from 448
-    # without.
+    # 128-query from 320 groups of 128.
     (1, 40, 1024, True, K.FA2_KERNEL_128_QUERY), (1, 72, 512, True, K.FA2_KERNEL_KEY_SPLIT_32),
-    (1, 57, 1024, True, K.FA2_KERNEL_128_QUERY), (1, 55, 1024, True, K.FA2_KERNEL_KEY_SPLIT_32),
-    (1, 12, 4096, True, K.FA2_KERNEL_KEY_SPLIT_32), (1, 24, 2048, True, K.FA2_KERNEL_128_QUERY),
+    (1, 57, 1024, True, K.FA2_KERNEL_128_QUERY), (1, 39, 1024, True, K.FA2_KERNEL_KEY_SPLIT_32),
+    (1, 12, 4096, True, K.FA2_KERNEL_128_QUERY), (1, 24, 2048, True, K.FA2_KERNEL_128_QUERY),
+    (1, 10, 4096, True, K.FA2_KERNEL_128_QUERY), (1, 8, 4096, True, K.FA2_KERNEL_KEY_SPLIT_32),
     (1, 8, 1024, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16), (1, 2, 128, True, K.FA2_KERNEL_KEY_SPLIT_64),
     (1, 8, 896, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16), (1, 2, 1024, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16),
     (1, 8, 512, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16), (1, 8, 384, True, K.FA2_KERNEL_KEY_SPLIT_64),

@@ -6,11 +6,10 @@ ends in a partial round that the 128-query kernel's finer rounds finish sooner; 
 one query tile per workgroup in per-XCD head groups when batch*heads is a multiple of 8
 and a head has at least 8 tiles or the grid 2048; else pairs of query tiles when a head
 has an even number of them, one tile per workgroup from 2048 when odd), the 128-query
-kernel from 256 (noncausal) or 320 (causal with batch*heads a multiple of 8, else 448)
-groups of 128 queries, and otherwise the key-split kernel: up to 256 query blocks of
-32, 4 waves with 64-key tiles (noncausal from 1024 keys with dedicated DMA waves; causal
-from 512 to 2047 keys, pairs of 16-query blocks; 8 waves with 32-key tiles from 2048
-keys on), and 32-key tiles
+kernel from 256 (noncausal) or 320 (causal) groups of 128 queries, and otherwise the
+key-split kernel: up to 256 query blocks of 32, 4 waves with 64-key tiles (noncausal
+from 1024 keys with dedicated DMA waves; causal from 512 to 2047 keys, pairs of 16-query
+blocks; 8 waves with 32-key tiles from 2048 keys on), and 32-key tiles
 beyond. Each case below sits one step below or at a threshold, and `fa2_forward_plan`
 (the function the forward dispatches through) must name the kernel the case is meant
 to reach; every row of the first and last head and sampled rows of the others are
@@ -51,8 +50,8 @@ CASES = [
     (1, 256, 1024, True, "256-query, tile pairs (512 pairs)", K.FA2_KERNEL_256_QUERY_PAIRS),
     (1, 409, 1280, True, "128-query (2045 single tiles, odd count per head)", K.FA2_KERNEL_128_QUERY),
     (1, 410, 1280, True, "256-query, single tiles (2050, odd count per head)", K.FA2_KERNEL_256_QUERY),
-    (1, 55, 1024, True, "key-split, 32-key tiles (440 groups of 128, no head groups)", K.FA2_KERNEL_KEY_SPLIT_32),
-    (1, 57, 1024, True, "128-query (456 groups of 128, no head groups)", K.FA2_KERNEL_128_QUERY),
+    (1, 39, 1024, True, "key-split, 32-key tiles (312 groups of 128)", K.FA2_KERNEL_KEY_SPLIT_32),
+    (1, 57, 1024, True, "128-query (456 groups of 128, heads split across XCDs)", K.FA2_KERNEL_128_QUERY),
     (1, 72, 512, True, "key-split, 32-key tiles (288 groups of 128)", K.FA2_KERNEL_KEY_SPLIT_32),
     (1, 40, 1024, True, "128-query (320 groups of 128, head groups)", K.FA2_KERNEL_128_QUERY),
     (1, 64, 1024, True, "128-query (512 groups of 128)", K.FA2_KERNEL_128_QUERY),

@@ -166,12 +166,18 @@ __device__ __forceinline__ uint32_t group_heads(uint32_t tiles_per_head) {
 // Dispatch is round-robin over the 8 XCDs (id % 8), so every XCD gets a contiguous
 // range of logical (head-major) items and the items of one head share that XCD's L2.
 // `item` counts from the heaviest (item 0 = the last query tile of a head).
-// Noncausal: the XCD's range in order. Causal: the range in chunks of group_heads(T)
-// heads' worth of items, each chunk in level order (every head's item 0, then every
-// head's item 1, ...). When batch_heads is a multiple of 8 the chunks are whole heads:
-// the head groups above. Otherwise the XCD ranges split heads, and a chunk's first and
-// last head may contribute only some levels; a binary search over the levels finds the
-// slot's level from the count of the chunk's items below each level.
+// Noncausal: the XCD's range in order. Causal: the range in level order (every head's
+// item 0, then every head's item 1, ...), chunk by chunk when the range divides into
+// chunks of group_heads(T) heads' worth of items (the head groups above when
+// batch_heads is a multiple of 8), else as one chunk: a short last chunk would hold
+// heavy items that start only after the earlier chunks have filled the slots. Where
+// the XCD ranges split heads, a chunk's first and last head contribute only some
+// levels; a binary search over the levels finds the slot's level from the count of
+// the chunk's items below each level. Measured on MI355X (same process, bit-identical,
+// fixed-size chunks -> this): -20% to -32% at B1 H66 N4096, B1 H72 N4096, B1 H80
+// N4096, B1 H130 N2048, B1 H36 N4096, B1 H40 N4096. One chunk per XCD everywhere
+// instead cost 1-3% where the chunks are whole (B16 H16 N4096, B1 H64 N4096): the
+// XCD's L2 then holds more heads' K/V at once.
 struct WorkItem {
     uint32_t bh, item;
 };
@@ -189,12 +195,13 @@ __device__ __forceinline__ WorkItem xcd_work_item(uint32_t tiles_per_head) {
         const uint32_t bh = logical / T;
         return {bh, logical - bh * T};
     }
-    const uint32_t xcd_end = xcd_begin + per_xcd + (xcd < extra ? 1u : 0u);
-    const uint32_t chunk_items = group_heads(T) * T;
+    const uint32_t count = per_xcd + (xcd < extra ? 1u : 0u);
+    const uint32_t group_items = group_heads(T) * T;
+    const uint32_t chunk_items = count % group_items == 0 ? group_items : count;
     const uint32_t chunk = slot / chunk_items;
     const uint32_t begin = xcd_begin + chunk * chunk_items;
-    const uint32_t end = min(begin + chunk_items, xcd_end);  // exclusive; the last chunk may be short
-    const uint32_t rank = slot - chunk * chunk_items;        // position in level order
+    const uint32_t end = begin + chunk_items;  // exclusive
+    const uint32_t rank = slot - chunk * chunk_items;  // position in level order
     const uint32_t head_first = begin / T, level_first = begin - head_first * T;  // its levels >= level_first
     const uint32_t head_last = (end - 1) / T, level_last = (end - 1) - head_last * T;  // its levels <= level_last
     // Items of the chunk on levels below k.
@@ -2074,15 +2081,19 @@ hipError_t launch_wide(const void* q, const void* k, const void* v, void* o, int
     return hipGetLastError();
 }
 
-// Causal 256-query problems run one query tile per workgroup in the head-group order
-// when every XCD owns whole heads (batch*heads a multiple of 8) and the grid has
-// enough tiles to balance; otherwise pairs of tiles (T even). Measured on MI355X
-// (same process, pairs -> head groups): -4% to -5% at 1024 tiles with T >= 8
-// (B8 H16 N2048, B4 H16 N4096, B1 H64 N4096), -2% to -4% at 2048 tiles (B32 H16 N1024,
-// B16 H16 N2048, B8 H16 N4096), -1% to -3% at 4096 (B16 H16 N4096, B2 H32 N16384);
-// +2% at B16 H16 N1024 (1024 tiles of T = 4).
+// Causal 256-query problems run one query tile per workgroup in the level order of
+// xcd_work_item when the grid has enough tiles to balance and the XCDs get about
+// equal work; otherwise pairs of tiles (T even), which give every workgroup the same
+// work. Measured on MI355X (same process, pairs -> head groups): -4% to -5% at 1024
+// tiles with T >= 8 (B8 H16 N2048, B4 H16 N4096, B1 H64 N4096), -2% to -4% at 2048
+// tiles (B32 H16 N1024, B16 H16 N2048, B8 H16 N4096), -1% to -3% at 4096 (B16 H16
+// N4096, B2 H32 N16384); +2% at B16 H16 N1024 (1024 tiles of T = 4). When batch*heads
+// is not a multiple of 8 the XCD ranges split heads, and an XCD whose range holds a
+// split head's heavy tiles gets more work: up to 8/batch_heads of a head's share more
+// (5.5% at 36 heads; 82% for one head), so single tiles need 32 heads or more there:
+// -28% to -32% at B1 H66 N4096 and B1 H130 N2048 (with the level order).
 bool use_head_groups(int64_t batch_heads, int64_t tiles_per_head) {
-    if (batch_heads % 8 != 0) return false;
+    if (batch_heads % 8 != 0 && batch_heads < 32) return false;
     return tiles_per_head >= 8 || batch_heads * tiles_per_head >= 2048;
 }
 

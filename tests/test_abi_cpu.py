@@ -62,13 +62,12 @@ K = capi
     (7, 16, 2048, False, K.FA2_KERNEL_256_QUERY), (6, 16, 4096, False, K.FA2_KERNEL_256_QUERY),
     # Causal: 256-query from 512 workgroups of tile pairs when a head has an even
     # number T of tiles, single tiles from 2048 with an odd number. Single tiles in
-    # head groups (batch*heads a multiple of 8) from T >= 8 or 2048 tiles; pairs below
-    # that and when batch*heads is not a multiple of 8.
+    # level order from T >= 8 or 2048 tiles; pairs below that.
     (16, 16, 4096, True, K.FA2_KERNEL_256_QUERY), (1, 256, 1024, True, K.FA2_KERNEL_256_QUERY_PAIRS),
     (1, 255, 1024, True, K.FA2_KERNEL_128_QUERY), (2, 32, 16384, True, K.FA2_KERNEL_256_QUERY),
     (32, 16, 1024, True, K.FA2_KERNEL_256_QUERY), (1, 504, 1024, True, K.FA2_KERNEL_256_QUERY_PAIRS),
     (8, 16, 2048, True, K.FA2_KERNEL_256_QUERY), (1, 64, 4096, True, K.FA2_KERNEL_256_QUERY),
-    (1, 66, 4096, True, K.FA2_KERNEL_256_QUERY_PAIRS), (1, 510, 1024, True, K.FA2_KERNEL_256_QUERY_PAIRS),
+    (1, 66, 4096, True, K.FA2_KERNEL_256_QUERY), (1, 510, 1024, True, K.FA2_KERNEL_256_QUERY_PAIRS),
     (1, 410, 1280, True, K.FA2_KERNEL_256_QUERY), (1, 409, 1280, True, K.FA2_KERNEL_128_QUERY),
     (1, 64, 1024, True, K.FA2_KERNEL_128_QUERY),
     # 128-query from 320 groups of 128.

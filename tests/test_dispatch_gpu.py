@@ -3,8 +3,8 @@
 The forward picks its kernel from (batch*heads, seq_len, causal) (fa2_forward.hip,
 `choose_kernel`): the 256-query kernel from 512 workgroups (noncausal: unless its grid
 ends in a partial round that the 128-query kernel's finer rounds finish sooner; causal:
-one query tile per workgroup in per-XCD head groups when batch*heads is a multiple of 8
-and a head has at least 8 tiles or the grid 2048; else pairs of query tiles when a head
+one query tile per workgroup in level order (per-XCD head groups when batch*heads is a
+multiple of 8) when a head has at least 8 tiles or the grid 2048; else pairs of query tiles when a head
 has an even number of them, one tile per workgroup from 2048 when odd), the 128-query
 kernel from 256 (noncausal) or 320 (causal) groups of 128 queries, and otherwise the
 key-split kernel: up to 256 query blocks of 32, 4 waves with 64-key tiles (noncausal
@@ -72,7 +72,7 @@ CASES = [
     (1, 504, 1024, True, "256-query, tile pairs (2016 tiles of T = 4)", K.FA2_KERNEL_256_QUERY_PAIRS),
     (32, 16, 1024, True, "256-query, head groups (2048 tiles of T = 4)", K.FA2_KERNEL_256_QUERY),
     (1, 64, 4096, True, "256-query, head groups (1024 tiles of T = 16)", K.FA2_KERNEL_256_QUERY),
-    (1, 66, 4096, True, "256-query, tile pairs (batch*heads not a multiple of 8)", K.FA2_KERNEL_256_QUERY_PAIRS),
+    (1, 66, 4096, True, "256-query, single tiles (XCD ranges splitting heads)", K.FA2_KERNEL_256_QUERY),
 ]
 
 

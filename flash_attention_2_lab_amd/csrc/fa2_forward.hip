@@ -697,9 +697,10 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_splitk_kernel(const _
     const int half = lane >> 5;
 
     // Workgroup -> (batch*head, query block): XCD-contiguous, head by head, causal
-    // blocks heaviest first. (Head groups, as in the 128-query kernel, measured -1% to
-    // -3% at B1 H32 N1024 and B4 H8 N1024 but +6% to +10% at B1 H40 N1024 and B1 H24
-    // N1024: these grids are at most a few rounds of short workgroups.)
+    // blocks heaviest first. (The 128-query kernel's level order measured 0 to +4% at
+    // B1 H24 N1024, B1 H32 N1024, B4 H8 N1024, B1 H16 N2048, B1 H12 N2048 and -4% at
+    // B1 H36 N1024: these grids are a few rounds of short workgroups whose keys are
+    // already split over four waves.)
     const WorkItem work = xcd_work_item<false>((uint32_t)num_query_blocks);
     const uint32_t bh = work.bh;
     const uint32_t qblock = kCausal ? (uint32_t)num_query_blocks - 1u - work.item : work.item;

@@ -76,34 +76,29 @@ CASES = [
 ]
 
 
-KERNEL_IDS = (K.FA2_KERNEL_128_QUERY, K.FA2_KERNEL_256_QUERY, K.FA2_KERNEL_256_QUERY_PAIRS,
-              K.FA2_KERNEL_KEY_SPLIT_64, K.FA2_KERNEL_KEY_SPLIT_32, K.FA2_KERNEL_KEY_SPLIT_8_WAVES,
-              K.FA2_KERNEL_KEY_SPLIT_PAIRS16, K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES)
-
-
-def _random_shapes(per_kernel, seed):
+def _random_shapes(per_route, seed):
     # (batch, heads, seq_len, causal) drawn from one seeded stream: seq_len a multiple of
     # 128 up to 4096, batch*heads log-uniform from 1 to 576, at most 576 heads of 1024
-    # keys' worth of work. The first `per_kernel` draws that each kernel runs are kept,
-    # so every kernel of the routing table is checked on shapes nobody picked by hand.
+    # keys' worth of work. The first `per_route` draws for each (kernel, mode) that the
+    # routing table can produce are kept, so every kernel and schedule is checked on
+    # shapes nobody picked by hand.
     gen = torch.Generator().manual_seed(seed)
-    picked = {kernel: [] for kernel in KERNEL_IDS}
-    for _ in range(20000):
-        if all(len(v) == per_kernel for v in picked.values()):
-            break
+    picked = {}
+    for _ in range(40000):
         seq_len = 128 * int(torch.randint(1, 33, (1,), generator=gen))
         batch = int(torch.randint(1, 5, (1,), generator=gen))
         heads = max(1, round(math.exp(float(torch.rand(1, generator=gen)) * math.log(576 / batch))))
         causal = bool(torch.randint(0, 2, (1,), generator=gen))
         if batch * heads * seq_len > 576 * 1024:
             continue
-        kernel = capi.forward_plan(batch, heads, seq_len, causal)
-        if len(picked[kernel]) < per_kernel:
-            picked[kernel].append((batch, heads, seq_len, causal))
-    return [shape for kernel in KERNEL_IDS for shape in picked[kernel]]
+        route = (capi.forward_plan(batch, heads, seq_len, causal), causal)
+        shapes = picked.setdefault(route, [])
+        if len(shapes) < per_route:
+            shapes.append((batch, heads, seq_len, causal))
+    return [shape for route in sorted(picked) for shape in picked[route]]
 
 
-RANDOM_SHAPES = _random_shapes(4, seed=2024)
+RANDOM_SHAPES = _random_shapes(3, seed=2024)
 
 
 def _inputs(batch, heads, seq_len, seed):

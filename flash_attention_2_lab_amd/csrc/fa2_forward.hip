@@ -2185,6 +2185,13 @@ fa2_forward_kernel choose_kernel(int64_t batch_heads, int64_t seq_len, bool caus
     // key-split kernel: -4% to -5% at B1 H8 N1024 and B1 H1 N1024; below 1024 keys
     // (one to three tiles per wave) it was 3-9% slower.
     if (!causal && seq_len >= kDmaWavesMinKeys) return FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES;
+    // Otherwise 4 waves with 64-key tiles when each wave gets the same number of them;
+    // else 32-key tiles, which split the keys evenly (or less unevenly) and give short
+    // causal blocks more waves. Measured on MI355X (same process, graph replays, 64- ->
+    // 32-key tiles): noncausal -6% at N128, -7% at N384, -6% at N640, -3% to -5% at N896
+    // (B1 H2-H8), 0 at N256, N512, N768; causal -14% at N128, -5% to -8% at N256, -13%
+    // at N384.
+    if (causal || ((seq_len + kKeysPerTile - 1) / kKeysPerTile) % 4 != 0) return FA2_KERNEL_KEY_SPLIT_32;
     return FA2_KERNEL_KEY_SPLIT_64;
 }
 

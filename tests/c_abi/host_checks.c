@@ -171,7 +171,8 @@ int main(void) {
     CHECK(fa2_matmul_16x64x16_f16(fake[0] + 1, fake[1], fo, 1, NULL) == FA2_STATUS_MISALIGNED, "matmul misaligned");
 
     CHECK(fa2_forward_plan(1, 8, 1024, 0) == FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES, "plan bench size");
-    CHECK(fa2_forward_plan(1, 8, 896, 0) == FA2_KERNEL_KEY_SPLIT_64, "plan below 1024 keys");
+    CHECK(fa2_forward_plan(1, 8, 768, 0) == FA2_KERNEL_KEY_SPLIT_64, "plan below 1024 keys");
+    CHECK(fa2_forward_plan(1, 8, 896, 0) == FA2_KERNEL_KEY_SPLIT_32, "plan with an uneven 64-key split");
     CHECK(fa2_forward_plan(16, 16, 4096, 0) == FA2_KERNEL_256_QUERY, "plan throughput size");
     CHECK(fa2_forward_plan(16, 16, 4096, 1) == FA2_KERNEL_256_QUERY, "plan throughput size causal");
     CHECK(fa2_forward_plan(16, 16, 1024, 1) == FA2_KERNEL_256_QUERY_PAIRS, "plan causal pairs");

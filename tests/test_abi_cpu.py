@@ -54,7 +54,7 @@ K = capi
     (1, 128, 1024, False, K.FA2_KERNEL_256_QUERY), (1, 127, 1024, False, K.FA2_KERNEL_128_QUERY),
     (16, 16, 4096, False, K.FA2_KERNEL_256_QUERY), (1, 32, 1024, False, K.FA2_KERNEL_128_QUERY),
     (1, 31, 1024, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 8, 1024, False, K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES),
-    (1, 9, 1024, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 8, 128, False, K.FA2_KERNEL_KEY_SPLIT_64),
+    (1, 9, 1024, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 8, 128, False, K.FA2_KERNEL_KEY_SPLIT_32),
     # ... except where the 256-query grid ends in a last round at most half full and
     # the 128-query kernel's finer rounds are modeled more than 5% faster.
     (1, 36, 4096, False, K.FA2_KERNEL_128_QUERY), (5, 16, 2048, False, K.FA2_KERNEL_128_QUERY),
@@ -75,21 +75,21 @@ K = capi
     (1, 57, 1024, True, K.FA2_KERNEL_128_QUERY), (1, 39, 1024, True, K.FA2_KERNEL_KEY_SPLIT_32),
     (1, 12, 4096, True, K.FA2_KERNEL_128_QUERY), (1, 24, 2048, True, K.FA2_KERNEL_128_QUERY),
     (1, 10, 4096, True, K.FA2_KERNEL_128_QUERY), (1, 8, 4096, True, K.FA2_KERNEL_KEY_SPLIT_32),
-    (1, 8, 1024, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16), (1, 2, 128, True, K.FA2_KERNEL_KEY_SPLIT_64),
+    (1, 8, 1024, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16), (1, 2, 128, True, K.FA2_KERNEL_KEY_SPLIT_32),
     (1, 8, 896, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16), (1, 2, 1024, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16),
-    (1, 8, 512, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16), (1, 8, 384, True, K.FA2_KERNEL_KEY_SPLIT_64),
-    (1, 8, 544, True, K.FA2_KERNEL_KEY_SPLIT_64),
-    (1, 4, 1920, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16), (1, 4, 1040, True, K.FA2_KERNEL_KEY_SPLIT_64),
+    (1, 8, 512, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16), (1, 8, 384, True, K.FA2_KERNEL_KEY_SPLIT_32),
+    (1, 8, 544, True, K.FA2_KERNEL_KEY_SPLIT_32),
+    (1, 4, 1920, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16), (1, 4, 1040, True, K.FA2_KERNEL_KEY_SPLIT_32),
     # Key-split shapes from 2048 keys on split each block's keys over 8 waves.
     (1, 2, 4096, False, K.FA2_KERNEL_KEY_SPLIT_8_WAVES), (1, 1, 2048, True, K.FA2_KERNEL_KEY_SPLIT_8_WAVES),
     (1, 4, 2048, False, K.FA2_KERNEL_KEY_SPLIT_8_WAVES), (1, 1, 8192, True, K.FA2_KERNEL_KEY_SPLIT_8_WAVES),
     (1, 4, 1024, False, K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES), (1, 8, 2048, True, K.FA2_KERNEL_KEY_SPLIT_32),
-    (1, 8, 896, False, K.FA2_KERNEL_KEY_SPLIT_64), (1, 4, 1920, False, K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES),
+    (1, 8, 896, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 8, 768, False, K.FA2_KERNEL_KEY_SPLIT_64), (1, 4, 1920, False, K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES),
     (1, 4, 1040, False, K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES), (1, 2, 2000, False, K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES),
     (1, 1, 2064, False, K.FA2_KERNEL_KEY_SPLIT_8_WAVES),
     # Sequence lengths the production entry rejects but the Bc16/Bc32 entries take
     # (partial last block) run the key-split kernel.
-    (4, 64, 1040, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 2, 80, False, K.FA2_KERNEL_KEY_SPLIT_64),
+    (4, 64, 1040, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 2, 80, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 2, 240, False, K.FA2_KERNEL_KEY_SPLIT_64),
     # Nothing to launch.
     (0, 8, 1024, False, K.FA2_KERNEL_NONE), (1, 0, 1024, True, K.FA2_KERNEL_NONE),
     (1, 8, 0, False, K.FA2_KERNEL_NONE), (1, 1, (1 << 24) + 128, False, K.FA2_KERNEL_NONE),

@@ -275,14 +275,17 @@ def test_growing_scores_match_oracle(shape, causal):
     _assert_close_to_oracle(out, attention_reference_fp32(q, k, v, causal=causal))
 
 
-@pytest.mark.parametrize("shape", [(1, 4, 2000), (1, 2, 2064), (1, 4, 880)])
+@pytest.mark.parametrize("shape", [(1, 4, 2000), (1, 2, 2064), (1, 4, 880), (1, 4, 496)])
 def test_growing_scores_on_partial_key_tiles(shape):
     # The partial-tile key-split instantiations (sequence lengths that are multiples of
-    # 16 only, through the Bc16 entry): 64-key tiles below 1024 keys, with DMA waves
+    # 16 only, through the Bc16 entry): below 1024 keys 64- or 32-key tiles (496 keys:
+    # 8 tiles of 64; 880 keys: 32-key tiles, 14 of 64 would split unevenly over the
+    # waves), with DMA waves
     # from 1024, 8 waves with 32-key tiles from 2048 on, keys masked past the end.
     # Ramped key norms force the exact-max recompute on the partial tiles too.
     batch, heads, seq_len = shape
     assert capi.forward_plan(batch, heads, seq_len, False) in (capi.FA2_KERNEL_KEY_SPLIT_64,
+                                                               capi.FA2_KERNEL_KEY_SPLIT_32,
                                                                capi.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES,
                                                                capi.FA2_KERNEL_KEY_SPLIT_8_WAVES)
     q, k, v = _inputs(batch, heads, seq_len, seed=19)

@@ -4,12 +4,13 @@ The forward picks its kernel from (batch*heads, seq_len, causal) (fa2_forward.hi
 `choose_kernel`): the 256-query kernel from 512 workgroups (noncausal: unless its grid
 ends in a partial round that the 128-query kernel's finer rounds finish sooner; causal:
 one query tile per workgroup in level order (per-XCD head groups when batch*heads is a
-multiple of 8) when a head has at least 8 tiles or the grid 2048; else pairs of query tiles when a head
-has an even number of them, one tile per workgroup from 2048 when odd), the 128-query
-kernel from 256 (noncausal) or 320 (causal) groups of 128 queries, and otherwise the
-key-split kernel: up to 256 query blocks of 32, 4 waves with 64-key tiles (noncausal
-from 1024 keys with dedicated DMA waves; causal from 512 to 2047 keys, pairs of 16-query
-blocks; 8 waves with 32-key tiles from 2048 keys on), and 32-key tiles
+multiple of 8) when a head has at least 8 tiles or the grid 2048; else pairs of query
+tiles when a head has an even number of them, one tile per workgroup from 2048 when odd),
+the 128-query kernel from 256 (noncausal) or 320 (causal) groups of 128 queries, and
+otherwise the key-split kernel: up to 256 query blocks of 32, 4 waves with 64-key tiles
+(noncausal from 1024 keys with dedicated DMA waves; causal from 512 to 2047 keys, pairs of
+16-query blocks; 8 waves with 32-key tiles from 2048 keys on; 32-key tiles when 64-key
+tiles would split unevenly over the waves, and causal below 512 keys), and 32-key tiles
 beyond. Each case below sits one step below or at a threshold, and `fa2_forward_plan`
 (the function the forward dispatches through) must name the kernel the case is meant
 to reach; every row of the first and last head and sampled rows of the others are
@@ -42,7 +43,8 @@ CASES = [
     (1, 31, 1024, False, "key-split, 32-key tiles (248 groups of 128)", K.FA2_KERNEL_KEY_SPLIT_32),
     (1, 32, 1024, False, "128-query (256 groups of 128)", K.FA2_KERNEL_128_QUERY),
     (1, 8, 1024, False, "key-split, 64-key tiles, DMA waves (256 query blocks)", K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES),
-    (1, 8, 896, False, "key-split, 64-key tiles (224 blocks below 1024 keys)", K.FA2_KERNEL_KEY_SPLIT_64),
+    (1, 8, 768, False, "key-split, 64-key tiles (192 blocks, 12 tiles over 4 waves)", K.FA2_KERNEL_KEY_SPLIT_64),
+    (1, 8, 896, False, "key-split, 32-key tiles (224 blocks, 14 64-key tiles would split unevenly)", K.FA2_KERNEL_KEY_SPLIT_32),
     (1, 4, 1920, False, "key-split, 64-key tiles, DMA waves (the longest below 2048 keys)",
      K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES),
     (1, 9, 1024, False, "key-split, 32-key tiles (288 query blocks)", K.FA2_KERNEL_KEY_SPLIT_32),
@@ -60,7 +62,7 @@ CASES = [
      K.FA2_KERNEL_KEY_SPLIT_PAIRS16),
     (1, 8, 896, True, "key-split, pairs of 16-query blocks (896 keys)", K.FA2_KERNEL_KEY_SPLIT_PAIRS16),
     (1, 8, 512, True, "key-split, pairs of 16-query blocks (the shortest, 512 keys)", K.FA2_KERNEL_KEY_SPLIT_PAIRS16),
-    (1, 8, 384, True, "key-split, 64-key tiles (below 512 keys)", K.FA2_KERNEL_KEY_SPLIT_64),
+    (1, 8, 384, True, "key-split, 32-key tiles (causal below 512 keys)", K.FA2_KERNEL_KEY_SPLIT_32),
     (1, 2, 1024, True, "key-split, pairs of 16-query blocks (64 pairs)", K.FA2_KERNEL_KEY_SPLIT_PAIRS16),
     (3, 3, 1024, True, "key-split, 32-key tiles (288 query blocks)", K.FA2_KERNEL_KEY_SPLIT_32),
     (1, 4, 1024, False, "key-split, 64-key tiles, DMA waves (1024 keys)", K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES),

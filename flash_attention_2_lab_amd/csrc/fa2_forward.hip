@@ -42,6 +42,7 @@
 #include <math.h>
 
 #include <type_traits>
+#include <atomic>
 
 #include "fa2_mi355x.h"
 
@@ -2002,6 +2003,34 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
     }  // pass
 }
 
+// Launches through hipModuleLaunchKernel on the kernel's function handle (from
+// hipGetFuncBySymbol, cached per device): measured 0.3-0.5 us less host time per
+// launch than hipLaunchKernelGGL, and small problems run eagerly are bound by the
+// host's launch rate. Every forward kernel takes the same arguments.
+using ForwardKernel = void (*)(const _Float16*, const _Float16*, const _Float16*, _Float16*, int, int, float);
+constexpr int kMaxDevices = 64;
+
+template <ForwardKernel kKernel>
+hipError_t launch_kernel(unsigned grid, unsigned block, hipStream_t stream, const void* q, const void* k,
+                         const void* v, void* o, int seq_len, int tiles, float scale_log2) {
+    static std::atomic<hipFunction_t> functions[kMaxDevices];
+    int device = 0;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) return err;
+    hipFunction_t function = device < kMaxDevices ? functions[device].load(std::memory_order_acquire) : nullptr;
+    if (function == nullptr) {
+        err = hipGetFuncBySymbol(&function, reinterpret_cast<const void*>(kKernel));
+        if (err != hipSuccess) return err;
+        if (device < kMaxDevices) functions[device].store(function, std::memory_order_release);
+    }
+    const _Float16* qh = static_cast<const _Float16*>(q);
+    const _Float16* kh = static_cast<const _Float16*>(k);
+    const _Float16* vh = static_cast<const _Float16*>(v);
+    _Float16* oh = static_cast<_Float16*>(o);
+    void* params[] = {&qh, &kh, &vh, &oh, &seq_len, &tiles, &scale_log2};
+    return hipModuleLaunchKernel(function, grid, 1, 1, block, 1, 1, 0, stream, params, nullptr);
+}
+
 // kPartial instantiations (seq_len not a multiple of the 64-key tile) carry the
 // bounds checks of a partial last query block and key tile; the others have none.
 template <bool kCausal, int kSplit, int kBlocks>
@@ -2009,19 +2038,12 @@ hipError_t launch_splitk(const void* q, const void* k, const void* v, void* o,
                          int64_t batch_heads, int64_t seq_len, float scale_log2,
                          hipStream_t stream) {
     const int64_t query_blocks = (seq_len + kQueriesPerWave - 1) / kQueriesPerWave;
-    const dim3 grid((unsigned)(batch_heads * query_blocks));
-    const dim3 block(kSplit * 64);
-    const auto* qh = static_cast<const _Float16*>(q);
-    const auto* kh = static_cast<const _Float16*>(k);
-    const auto* vh = static_cast<const _Float16*>(v);
-    auto* oh = static_cast<_Float16*>(o);
+    const unsigned grid = (unsigned)(batch_heads * query_blocks);
     if (seq_len % (32 * kBlocks) != 0)
-        hipLaunchKernelGGL((fa2_forward_splitk_kernel<kCausal, true, kSplit, kBlocks>), grid, block, 0,
-                           stream, qh, kh, vh, oh, (int)seq_len, (int)query_blocks, scale_log2);
-    else
-        hipLaunchKernelGGL((fa2_forward_splitk_kernel<kCausal, false, kSplit, kBlocks>), grid, block, 0,
-                           stream, qh, kh, vh, oh, (int)seq_len, (int)query_blocks, scale_log2);
-    return hipGetLastError();
+        return launch_kernel<fa2_forward_splitk_kernel<kCausal, true, kSplit, kBlocks>>(
+            grid, kSplit * 64, stream, q, k, v, o, (int)seq_len, (int)query_blocks, scale_log2);
+    return launch_kernel<fa2_forward_splitk_kernel<kCausal, false, kSplit, kBlocks>>(
+        grid, kSplit * 64, stream, q, k, v, o, (int)seq_len, (int)query_blocks, scale_log2);
 }
 
 template <bool kCausal, int kSplit, int kBlocks>
@@ -2029,30 +2051,20 @@ hipError_t launch_splitk_dma_waves(const void* q, const void* k, const void* v, 
                                    int64_t batch_heads, int64_t seq_len, float scale_log2,
                                    hipStream_t stream) {
     const int64_t query_blocks = (seq_len + kQueriesPerWave - 1) / kQueriesPerWave;
-    const dim3 grid((unsigned)(batch_heads * query_blocks));
-    const dim3 block(2 * kSplit * 64);
-    const auto* qh = static_cast<const _Float16*>(q);
-    const auto* kh = static_cast<const _Float16*>(k);
-    const auto* vh = static_cast<const _Float16*>(v);
-    auto* oh = static_cast<_Float16*>(o);
+    const unsigned grid = (unsigned)(batch_heads * query_blocks);
     if (seq_len % (32 * kBlocks) != 0)
-        hipLaunchKernelGGL((fa2_forward_splitk_dma_waves_kernel<kCausal, true, kSplit, kBlocks>), grid, block, 0,
-                           stream, qh, kh, vh, oh, (int)seq_len, (int)query_blocks, scale_log2);
-    else
-        hipLaunchKernelGGL((fa2_forward_splitk_dma_waves_kernel<kCausal, false, kSplit, kBlocks>), grid, block, 0,
-                           stream, qh, kh, vh, oh, (int)seq_len, (int)query_blocks, scale_log2);
-    return hipGetLastError();
+        return launch_kernel<fa2_forward_splitk_dma_waves_kernel<kCausal, true, kSplit, kBlocks>>(
+            grid, 2 * kSplit * 64, stream, q, k, v, o, (int)seq_len, (int)query_blocks, scale_log2);
+    return launch_kernel<fa2_forward_splitk_dma_waves_kernel<kCausal, false, kSplit, kBlocks>>(
+        grid, 2 * kSplit * 64, stream, q, k, v, o, (int)seq_len, (int)query_blocks, scale_log2);
 }
 
 template <int kSplit>
 hipError_t launch_pairs16(const void* q, const void* k, const void* v, void* o, int64_t batch_heads,
                           int64_t seq_len, float scale_log2, hipStream_t stream) {
     const int64_t pairs = seq_len / 32;  // 16-query blocks per head, paired
-    hipLaunchKernelGGL((fa2_forward_pairs16_kernel<kSplit>), dim3((unsigned)(batch_heads * pairs)),
-                       dim3(kSplit * 64), 0, stream, static_cast<const _Float16*>(q),
-                       static_cast<const _Float16*>(k), static_cast<const _Float16*>(v),
-                       static_cast<_Float16*>(o), (int)seq_len, (int)pairs, scale_log2);
-    return hipGetLastError();
+    return launch_kernel<fa2_forward_pairs16_kernel<kSplit>>((unsigned)(batch_heads * pairs), kSplit * 64, stream,
+                                                             q, k, v, o, (int)seq_len, (int)pairs, scale_log2);
 }
 
 template <bool kCausal, int kWaves>
@@ -2061,13 +2073,9 @@ hipError_t launch_forward(const void* q, const void* k, const void* v, void* o,
                           hipStream_t stream) {
     const int64_t block_m = (int64_t)kWaves * kQueriesPerWave;
     const int64_t query_tiles = seq_len / block_m;
-    const int64_t groups = batch_heads * query_tiles;
-    hipLaunchKernelGGL((fa2_forward_d64_kernel<kCausal, kWaves>), dim3((unsigned)groups),
-                       dim3(kWaves * 64), 0, stream,
-                       static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
-                       static_cast<const _Float16*>(v), static_cast<_Float16*>(o),
-                       (int)seq_len, (int)query_tiles, scale_log2);
-    return hipGetLastError();
+    return launch_kernel<fa2_forward_d64_kernel<kCausal, kWaves>>((unsigned)(batch_heads * query_tiles), kWaves * 64,
+                                                                  stream, q, k, v, o, (int)seq_len, (int)query_tiles,
+                                                                  scale_log2);
 }
 
 template <bool kCausal, bool kPairs>
@@ -2075,13 +2083,10 @@ hipError_t launch_wide(const void* q, const void* k, const void* v, void* o, int
                        int64_t seq_len, float scale_log2, hipStream_t stream) {
     const int64_t query_tiles = seq_len / 256;
     const int64_t items = kPairs ? query_tiles / 2 : query_tiles;
-    hipLaunchKernelGGL((fa2_forward_d64_wide_kernel<kCausal, kPairs>), dim3((unsigned)(batch_heads * items)),
-                       dim3(256), 0, stream, static_cast<const _Float16*>(q), static_cast<const _Float16*>(k),
-                       static_cast<const _Float16*>(v), static_cast<_Float16*>(o), (int)seq_len,
-                       (int)query_tiles, scale_log2);
-    return hipGetLastError();
+    return launch_kernel<fa2_forward_d64_wide_kernel<kCausal, kPairs>>((unsigned)(batch_heads * items), 256, stream, q,
+                                                                       k, v, o, (int)seq_len, (int)query_tiles,
+                                                                       scale_log2);
 }
-
 // Causal 256-query problems run one query tile per workgroup in the level order of
 // xcd_work_item when the grid has enough tiles to balance and the XCDs get about
 // equal work; otherwise pairs of tiles (T even), which give every workgroup the same

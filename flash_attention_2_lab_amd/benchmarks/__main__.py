@@ -44,6 +44,8 @@ def build_parser() -> argparse.ArgumentParser:
     parser.add_argument("--peak-tflops", type=float, default=MI355X_FP16_DENSE_TFLOPS,
                         help="Peak used for the fraction-of-peak column.")
     parser.add_argument("--json", action="store_true", help="Also print one JSON line per kernel.")
+    parser.add_argument("--graph", action="store_true",
+                        help="Time replays of a HIP graph of each sample's calls (device kernels only).")
     return parser
 
 
@@ -55,7 +57,7 @@ def main(argv: list[str] | None = None) -> int:
         head_dimension=args.head_dim, dtype=DTYPES[args.dtype], causal=args.causal,
     )
     config = BenchmarkConfig(warmup_iterations=args.warmup, samples=args.samples,
-                             iterations_per_sample=args.iterations)
+                             iterations_per_sample=args.iterations, graph=args.graph)
     inputs = generate_attention_inputs(workload)
     flops = attention_flops(workload)
 
@@ -86,7 +88,7 @@ def main(argv: list[str] | None = None) -> int:
                               "p10_ms": result.p10_ms, "p90_ms": result.p90_ms,
                               "min_ms": result.minimum_ms, "max_ms": result.maximum_ms,
                               "tflops": result.median_tflops, "peak_fraction": peak_frac,
-                              "workload": workload.label}))
+                              "workload": workload.label, "graph": bool(args.graph and spec.on_device)}))
     baseline = next((r for r in results if r.kernel_name == "pytorch_sdpa"), None)
     if baseline is not None:
         print()

@@ -5,6 +5,12 @@ sample bracketed by device events (host clock for CPU operations); the per-call
 time of every sample feeds median, min, p10, p90 and max. Percentiles are the
 nearest-rank values at index round((n - 1) * fraction) of the sorted samples, the
 reference's definition, so the two harnesses report comparable statistics.
+
+With `graph` set (an addition of this harness, off by default), the
+`iterations_per_sample` calls are captured once in a HIP graph and every sample
+replays it between the events: the calls then run back to back on the device with
+no host launches between them, which measures the kernels where eager calls are
+bound by the host's launch rate.
 """
 
 from __future__ import annotations
@@ -22,6 +28,7 @@ class BenchmarkConfig:
     warmup_iterations: int = 25
     samples: int = 20
     iterations_per_sample: int = 100
+    graph: bool = False
 
 
 @dataclass(frozen=True)
@@ -46,15 +53,35 @@ def percentile(values: list[float], fraction: float) -> float:
     return ordered[round((len(ordered) - 1) * fraction)]
 
 
+def _capture(operation: Callable[[], object], iterations: int) -> torch.cuda.CUDAGraph:
+    # Lazy set-up (allocator, library handles) happens on a side stream before capture.
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        operation()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(iterations):
+            operation()
+    graph.replay()
+    torch.cuda.synchronize()
+    return graph
+
+
 def _time_samples(operation: Callable[[], object], config: BenchmarkConfig, on_device: bool) -> list[float]:
     times_ms: list[float] = []
     if on_device:
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
+        graph = _capture(operation, config.iterations_per_sample) if config.graph else None
         for _ in range(config.samples):
             start.record()
-            for _ in range(config.iterations_per_sample):
-                operation()
+            if graph is not None:
+                graph.replay()
+            else:
+                for _ in range(config.iterations_per_sample):
+                    operation()
             end.record()
             end.synchronize()
             times_ms.append(start.elapsed_time(end) / config.iterations_per_sample)

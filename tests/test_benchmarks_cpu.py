@@ -86,6 +86,9 @@ def test_cli_defaults_match_the_reference():
     args = build_parser().parse_args([])
     assert (args.batch, args.heads, args.query_length, args.key_length, args.head_dim) == (1, 8, 512, None, 64)
     assert (args.dtype, args.samples, args.iterations, args.warmup, args.causal) == ("float32", 20, 100, 25, False)
+    # This harness's additions are off by default: eager timing, as the reference's.
+    assert args.graph is False and args.json is False
+    assert build_parser().parse_args(["--graph"]).graph is True
 
 
 def test_host_timing_path_and_cpu_comparator():

@@ -28,6 +28,22 @@ def test_cli_times_the_tensorcore_entries(capsys):
         assert r["tflops"] > 0 and 0 < r["peak_fraction"] < 1
 
 
+def test_cli_times_graph_replays(capsys):
+    # --graph: each sample's calls captured once in a HIP graph and replayed between the
+    # events; the result is a positive per-call time for the production entry and for
+    # the device SDPA comparator.
+    status = main(["--dtype", "float16", "--heads", "8", "--query-length", "256", "--causal",
+                   "--samples", "3", "--iterations", "20", "--warmup", "2", "--json", "--graph",
+                   "--kernels", "tensorcore_production_128x128", "pytorch_sdpa"])
+    out = capsys.readouterr().out
+    assert status == 0
+    rows = {r["kernel"]: r for r in (json.loads(line) for line in out.splitlines() if line.startswith("{"))}
+    assert set(rows) == {"tensorcore_production_128x128", "pytorch_sdpa"}
+    for r in rows.values():
+        assert r["graph"] is True
+        assert 0 < r["p10_ms"] <= r["median_ms"] <= r["p90_ms"]
+
+
 def test_cli_reports_unsupported_and_unknown_kernels(capsys):
     assert main(["--dtype", "float16", "--query-length", "80", "--samples", "1", "--iterations", "1",
                  "--warmup", "0", "--kernels", "tensorcore_production_128x128"]) == 0

@@ -1634,10 +1634,11 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_pairs16_kernel(const 
 //    only one or two rounds of workgroups, where the group order has too few tiles
 //    to balance; the light pass re-reads keys that have left L2.
 // Heads per group for T query tiles per head (group_heads): 64 / T, from 1 to 8. Measured on
-// MI355X (same process): at T = 16 (B16 H16 N4096) groups of 4 run 2.6% faster than
-// groups of 8 and fetch 1.04x Q+K+V from HBM against 1.69x; at T = 64 (B2 H32 N16384)
-// one head per group fetches 1.13x against 6.9x for 8, within 1.3% of the fastest
-// group size.
+// MI355X (same process): at T = 16 (B16 H16 N4096) groups of 4 fetch 1.04x Q+K+V from HBM
+// against 1.69x for groups of 8; at T = 64 (B2 H32 N16384) one head per group fetches 1.13x
+// against 6.9x for 8. With the balanced wave blocks and the level order, 128 / T heads per
+// group ran between 4% faster and 1% slower than 64 / T on two boxes (B16 H16 N4096, B2 H16
+// N8192, B4 H16 N2048, B2 H32 N16384, B64 H16 N512), and 256 / T up to 2% slower.
 
 template <bool kCausal, bool kPairs>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))

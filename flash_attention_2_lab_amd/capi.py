@@ -38,6 +38,7 @@ FA2_KERNEL_KEY_SPLIT_32 = 5
 FA2_KERNEL_KEY_SPLIT_8_WAVES = 6
 FA2_KERNEL_KEY_SPLIT_PAIRS16 = 7
 FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES = 8
+FA2_KERNEL_128_QUERY_SPLIT_PAIRS = 9
 
 
 class Fa2Error(RuntimeError):

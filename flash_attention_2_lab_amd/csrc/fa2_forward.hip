@@ -2004,6 +2004,303 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
     }  // pass
 }
 
+// Causal problems whose 128-query grid fills the chip's workgroup slots about once,
+// with long key streams: a workgroup of 8 waves takes the pair of 128-query tiles
+// T-1-p (heavy) and p (light) of one head (T = N/128, even), and the pair's 2T+2 key
+// tiles of 64 are split evenly between two groups of 4 waves. Group 0 streams the heavy
+// tile's key tiles 0..T; group 1 the light tile's 2p+2, then the heavy tile's remaining
+// T-2p-1. Wave w of a group owns queries 32(w%4)..32(w%4)+31 of the tile it serves.
+// Each group has a 4-stage ring of its own (64 KiB), and both take T+1 steps with one
+// workgroup barrier each, so every wave runs the same barriers. A wave skips the
+// compute of a key tile that lies wholly past its queries (the light tile's last one
+// for waves 0-1, and group 1's heavy keys for waves 0-1 of the middle pair), and every
+// wave that computes a tile has a key in it for each of its queries. At the end group 1
+// hands its part of the heavy tile (O, m and l per lane) to group 0 through LDS:
+//   m = max(m0, m1),  l = l0 2^((m0 - m) c) + l1 2^((m1 - m) c),  O likewise,
+// and group 0 stores the merged tile. With one workgroup per CU every SIMD keeps two
+// waves for the same T+1 steps, where one query tile per workgroup left the CU of the
+// heaviest tile running it alone, one wave per SIMD.
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
+void fa2_forward_d64_split_pairs_kernel(const _Float16* __restrict__ query,
+                                        const _Float16* __restrict__ key,
+                                        const _Float16* __restrict__ value,
+                                        _Float16* __restrict__ output,
+                                        int seq_len, int num_query_tiles, float scale_log2) {
+    constexpr int kGroupWaves = 4;
+    constexpr int kStages = 4;
+    constexpr int kStageBytes = 2 * kTileBytes;
+    constexpr int kRingBytes = kStages * kStageBytes;
+    constexpr int kDmaPerTile = kStageBytes / 1024 / kGroupWaves;  // LDS-DMA instructions per wave
+    constexpr int kHandoffFloats = 34;                             // per lane: O (2 x 16), m, l
+    static_assert(kGroupWaves * kHandoffFloats * 64 * 4 <= 2 * kRingBytes, "the handoff fits the rings");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * kRingBytes];
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int group = wave >> 2;
+    const int gw = wave & 3;
+    const int lane = tid & 63;
+    const int lq = lane & 31;
+    const int half = lane >> 5;
+
+    const int T = num_query_tiles;
+    const WorkItem work = xcd_work_item<false>((uint32_t)T / 2u);
+    const int light = (int)work.item;
+    const int heavy = T - 1 - light;
+    const int light_tiles = 2 * light + 2;  // 64-key tiles of the light tile
+    const int steps = T + 1;                // 64-key tiles per group
+
+    const size_t head_offset = (size_t)work.bh * (size_t)seq_len * kHeadDim;
+    const __amdgpu_buffer_rsrc_t q_head = head_resource(query + head_offset, seq_len);
+    const u32x4 k_head = head_descriptor(key + head_offset, seq_len);
+    const u32x4 v_head = head_descriptor(value + head_offset, seq_len);
+    const __amdgpu_buffer_rsrc_t o_head = head_resource(output + head_offset, seq_len);
+
+    // Step s of this group: its key tile, and whether it serves the light tile.
+    auto on_light = [&](int s) { return group == 1 && s < light_tiles; };
+    auto key_tile = [&](int s) { return (group == 0 || s < light_tiles) ? s : T + 1 + (s - light_tiles); };
+
+    uint8_t* const ring = smem + group * kRingBytes;
+    const uint32_t ring_addr = lds_address(ring);
+    // n & 1 = gw & 1 for every instruction of the wave: one lane offset.
+    const int dma_off = dma_lane_offset(lane, gw & 1);
+    // The group's waves issue instructions n = gw + x * 4 of a tile's 16 (8 per
+    // matrix, 8 rows each) into stage s % 4 of the group's ring.
+    auto dma_step = [&](int s) {
+        const int kt = key_tile(s);
+        const uint32_t stage = ring_addr + (uint32_t)((s & (kStages - 1)) * kStageBytes);
+#pragma unroll
+        for (int x = 0; x < kDmaPerTile; ++x) {
+            const int n = gw + x * kGroupWaves;
+            const int m = n >> 3;
+            const int r0 = (n & 7) * 8;
+            dma16_asm(m ? v_head : k_head, stage + (uint32_t)(m * kTileBytes + r0 * kRowBytes), dma_off,
+                      kt * kTileBytes + r0 * kRowBytes);
+        }
+    };
+
+    const int k_row = key_of_mfma_row(lq);
+    const int k_swz = tile_swizzle(k_row);
+    int k_off[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) k_off[ks] = k_row * kRowBytes + (((2 * ks + half) ^ k_swz) << 4);
+    const int grp = lane >> 4;
+    const int i16 = lane & 15;
+    int v_off[2][2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int dblk = 0; dblk < 2; ++dblk) {
+            const int row = 8 * half + 4 * r + (i16 >> 2);
+            const int chunk = 4 * dblk + 2 * (grp & 1) + ((i16 & 3) >> 1);
+            v_off[r][dblk] = row * kRowBytes + ((chunk ^ tile_swizzle(row)) << 4) + 8 * (i16 & 1);
+        }
+    const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+
+    // First query of this wave's 32-query block in each tile.
+    const int q_heavy = heavy * 128 + gw * kQueriesPerWave;
+    const int q_light = light * 128 + gw * kQueriesPerWave;
+
+    // Q^T fragments (B operands of K Q^T): the first tile the group serves, and the
+    // heavy tile for group 1's second part.
+    f16x8 qf[4], qf_heavy[4];
+    const int q_start = group == 0 ? q_heavy : q_light;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        qf[ks] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(q_head, (q_start + lq) * kRowBytes + 32 * ks + 16 * half, 0, 0));
+        qf_heavy[ks] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(q_head, (q_heavy + lq) * kRowBytes + 32 * ks + 16 * half, 0, 0));
+    }
+    dma_step(0);
+    dma_step(1);
+    dma_step(2);  // steps = T + 1 >= 3
+
+    // Exact tile max and lazy rescale of l and O (bound 2^kRescaleLog2); returns
+    // whether the max moved.
+    auto exact_max_update = [&](const f32x16 (&s)[2], float& m_run, float& l_run, f32x16 (&o)[2]) -> bool {
+        float tile_max = -INFINITY;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int i = 0; i < 16; i += 2) tile_max = fmaxf(fmaxf(tile_max, s[b][i]), s[b][i + 1]);
+        tile_max = max_across_halves(tile_max);
+        const bool grow = tile_max * scale_log2 > m_run * scale_log2 + kRescaleLog2;
+        if (__builtin_amdgcn_ballot_w64(grow) == 0) return false;
+        const float m_new = fmaxf(m_run, tile_max);
+        const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
+        l_run *= alpha;
+#pragma unroll
+        for (int d = 0; d < 2; ++d)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[d][i] *= alpha;
+        m_run = m_new;
+        return true;
+    };
+    // FP16 probabilities against the running max as P.V B operands; returns the lane
+    // sum (pairs added in FP16, then v_dot2 against 1.0 into FP32).
+    auto tile_probs = [&](const f32x16 (&s)[2], float m_run, f16x8 (&pf)[2][2]) -> float {
+        const float m_scaled = m_run * scale_log2;
+        float sum = 0.0f;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            f16x2 pk[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                pk[q] = pack_rn(__builtin_amdgcn_exp2f(fmaf(s[b][2 * q], scale_log2, -m_scaled)),
+                                __builtin_amdgcn_exp2f(fmaf(s[b][2 * q + 1], scale_log2, -m_scaled)));
+                if (q & 1) sum = __builtin_amdgcn_fdot2(pk[q - 1] + pk[q], ones, sum, false);
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const f16x4 lo = __builtin_shufflevector(pk[4 * h], pk[4 * h + 1], 0, 1, 2, 3);
+                const f16x4 hi = __builtin_shufflevector(pk[4 * h + 2], pk[4 * h + 3], 0, 1, 2, 3);
+                pf[b][h] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            }
+        }
+        return sum;
+    };
+    // Scores past the diagonal set to -inf (register i of key block kb holds key
+    // 64t + 32kb + 16(i/8) + 8*half + i%8), by bit select on the sign of limit - offset.
+    auto mask_diagonal = [&](f32x16 (&s)[2], int query, int t) {
+        const int limit = query - t * kKeysPerTile - 8 * half;
+        constexpr uint32_t kNegInf = 0xff800000u;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int hi = 0; hi < 2; ++hi) {
+                int base = limit - (32 * kb + 16 * hi);
+                asm volatile("" : "+v"(base));
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int i = 8 * hi + j;
+                    const uint32_t mask = (uint32_t)((base - j) >> 31);
+                    s[kb][i] = __uint_as_float((mask & kNegInf) | (~mask & __float_as_uint(s[kb][i])));
+                }
+            }
+    };
+    // O / l of one 32-query block as FP16: accumulator i of d-block dblk holds dim
+    // 32*dblk + 8*(i/4) + 4*half + i%4 of the lane's query; 8-byte stores.
+    auto store_block = [&](const f32x16 (&o)[2], float l_lane, int q_first) {
+        const float inv_l = 1.0f / sum_across_halves(l_lane);
+        const int row = (q_first + lq) * kRowBytes;
+#pragma unroll
+        for (int dblk = 0; dblk < 2; ++dblk)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f16x2 a = pack_rn(o[dblk][4 * g + 0] * inv_l, o[dblk][4 * g + 1] * inv_l);
+                const f16x2 c = pack_rn(o[dblk][4 * g + 2] * inv_l, o[dblk][4 * g + 3] * inv_l);
+                const f16x4 v = __builtin_shufflevector(a, c, 0, 1, 2, 3);
+                __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), o_head,
+                                                      row + 2 * (32 * dblk + 8 * g + 4 * half), 0, 0);
+            }
+    };
+
+    f32x16 o[2];
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[d][i] = 0.0f;
+    float m_run = -INFINITY;  // running max of raw scores
+    float l_run = 0.0f;       // this lane's share of the denominator
+    bool fresh = true;        // no key tile computed yet for the current query tile
+
+    wait_dma_and_barrier<0>();
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) asm volatile("" ::"v"(qf[ks]), "v"(qf_heavy[ks]));
+
+    for (int s = 0; s < steps; ++s) {
+        if (s + 3 < steps) dma_step(s + 3);  // into the stage step s-1 used
+        if (group == 1 && s == light_tiles) {
+            // The light tile is complete: store it, and start the heavy tile's last keys.
+            store_block(o, l_run, q_light);
+#pragma unroll
+            for (int d = 0; d < 2; ++d)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[d][i] = 0.0f;
+            m_run = -INFINITY;
+            l_run = 0.0f;
+            fresh = true;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) qf[ks] = qf_heavy[ks];
+        }
+        const int kt = key_tile(s);
+        const int q_first = on_light(s) ? q_light : q_heavy;
+        if (kt * kKeysPerTile <= q_first + kQueriesPerWave - 1) {
+            const uint8_t* k_lds = ring + (s & (kStages - 1)) * kStageBytes;
+            const uint8_t* v_lds = k_lds + kTileBytes;
+            __builtin_amdgcn_s_setprio(1);
+            f16x8 kf[2][4];
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+                    kf[b][ks] = *reinterpret_cast<const f16x8*>(k_lds + b * 32 * kRowBytes + k_off[ks]);
+            f32x16 sc[2];
+            const f32x16 zero = {};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+                    sc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[b][ks], qf[ks], ks == 0 ? zero : sc[b], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_setprio(0);
+            f16x8 vf[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int row_base = (32 * (k >> 2) + 16 * ((k >> 1) & 1)) * kRowBytes;
+                const f16x4 v_lo = lds_read_transposed(v_lds + row_base + v_off[0][k & 1]);
+                const f16x4 v_hi = lds_read_transposed(v_lds + row_base + v_off[1][k & 1]);
+                vf[k] = __builtin_shufflevector(v_lo, v_hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            }
+            if (kt * kKeysPerTile + kKeysPerTile - 1 > q_first) mask_diagonal(sc, q_first + lq, kt);
+            const bool first = fresh;
+            fresh = false;
+            if (first) exact_max_update(sc, m_run, l_run, o);
+            f16x8 pf[2][2];
+            float sum = tile_probs(sc, m_run, pf);
+            if (!first && __builtin_amdgcn_ballot_w64(sum > kTileSumBound) != 0 && exact_max_update(sc, m_run, l_run, o))
+                sum = tile_probs(sc, m_run, pf);
+            l_run += sum;
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                o[k & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[k], pf[k >> 2][(k >> 1) & 1], o[k & 1], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_setprio(0);
+        }
+        // Wait for step s+1's tile (only later fetches may stay in flight); after the
+        // barrier every wave is done with step s's stage.
+        if (s + 3 < steps) wait_dma_and_barrier<2 * kDmaPerTile>();
+        else if (s + 2 < steps) wait_dma_and_barrier<kDmaPerTile>();
+        else wait_dma_and_barrier<0>();
+    }
+
+    // Every wave is past the last step's barrier with no fetch in flight: the rings
+    // are free for the handoff (per wave 34 floats x 64 lanes, lane-contiguous).
+    float* const handoff = reinterpret_cast<float*>(smem) + gw * (kHandoffFloats * 64);
+    if (group == 1) {
+#pragma unroll
+        for (int d = 0; d < 2; ++d)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) handoff[(16 * d + i) * 64 + lane] = o[d][i];
+        handoff[32 * 64 + lane] = m_run;
+        handoff[33 * 64 + lane] = l_run;
+    }
+    __syncthreads();
+    if (group == 0) {
+        const float m_other = handoff[32 * 64 + lane];
+        const float l_other = handoff[33 * 64 + lane];
+        const float m_new = fmaxf(m_run, m_other);
+        const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
+        const float alpha_other = __builtin_amdgcn_exp2f((m_other - m_new) * scale_log2);  // 0 when m_other = -inf
+#pragma unroll
+        for (int d = 0; d < 2; ++d)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[d][i] = o[d][i] * alpha + handoff[(16 * d + i) * 64 + lane] * alpha_other;
+        store_block(o, l_run * alpha + l_other * alpha_other, q_heavy);
+    }
+}
+
 // Launches through hipModuleLaunchKernel on the kernel's function handle (from
 // hipGetFuncBySymbol, cached per device): measured 0.3-0.5 us less host time per
 // launch than hipLaunchKernelGGL, and small problems run eagerly are bound by the
@@ -2088,6 +2385,13 @@ hipError_t launch_wide(const void* q, const void* k, const void* v, void* o, int
                                                                        k, v, o, (int)seq_len, (int)query_tiles,
                                                                        scale_log2);
 }
+hipError_t launch_split_pairs(const void* q, const void* k, const void* v, void* o, int64_t batch_heads,
+                              int64_t seq_len, float scale_log2, hipStream_t stream) {
+    const int64_t query_tiles = seq_len / 128;
+    return launch_kernel<fa2_forward_d64_split_pairs_kernel>((unsigned)(batch_heads * (query_tiles / 2)), 512, stream,
+                                                             q, k, v, o, (int)seq_len, (int)query_tiles, scale_log2);
+}
+
 // Causal 256-query problems run one query tile per workgroup in the level order of
 // xcd_work_item when the grid has enough tiles to balance and the XCDs get about
 // equal work; otherwise pairs of tiles (T even), which give every workgroup the same
@@ -2159,6 +2463,21 @@ bool use_128_query_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
     return groups >= (causal ? 320 : 256);
 }
 
+// Causal problems of 320 to 512 groups of 128 queries (one round of the 128-query
+// kernel) with long key streams: the split pairs (fa2_forward_d64_split_pairs_kernel,
+// one workgroup per CU, 160 to 256 of them). Measured on MI355X against the
+// 128-query kernel (same process, graph replays): -6% to -10% at 8192 keys (B1 H5-H8),
+// -13% to -16% at 16384 (B1 H3-H4, also with sigma = 2 logits), -16% at B1 H2 N32768;
+// -4.5% to +1% at 4096 keys (B1 H10-H16, B2 H8) and 1-14% slower at 256-2048 keys,
+// where its steps, without the 128-query kernel's overlap of one tile's score MFMAs
+// with the previous tile's softmax, cost more than the balance saves.
+constexpr int64_t kSplitPairsMinKeys = 8192;
+bool use_split_pairs_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
+    if (!causal || seq_len % 256 != 0 || seq_len < kSplitPairsMinKeys) return false;
+    const int64_t groups = batch_heads * (seq_len / 128);
+    return groups >= 320 && groups <= 512;
+}
+
 constexpr int64_t kSplitWideMaxBlocks = 256;
 constexpr int64_t kEightWaveMinKeys = 2048;
 constexpr int64_t kPairs16MinKeys = 512;
@@ -2171,6 +2490,7 @@ fa2_forward_kernel choose_kernel(int64_t batch_heads, int64_t seq_len, bool caus
         return causal && tiles % 2 == 0 && !use_head_groups(batch_heads, tiles) ? FA2_KERNEL_256_QUERY_PAIRS
                                                                                : FA2_KERNEL_256_QUERY;
     }
+    if (use_split_pairs_kernel(batch_heads, seq_len, causal)) return FA2_KERNEL_128_QUERY_SPLIT_PAIRS;
     if (seq_len % kQueryTileAlign == 0 && use_128_query_kernel(batch_heads, seq_len, causal))
         return FA2_KERNEL_128_QUERY;
     const int64_t query_blocks = (seq_len + kQueriesPerWave - 1) / kQueriesPerWave;
@@ -2241,6 +2561,9 @@ int forward(const void* query, const void* key, const void* value, void* output,
         case FA2_KERNEL_128_QUERY:
             err = causal ? launch_forward<true, 4>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
                          : launch_forward<false, 4>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
+            break;
+        case FA2_KERNEL_128_QUERY_SPLIT_PAIRS:
+            err = launch_split_pairs(query, key, value, output, batch_heads, seq_len, scale_log2, s);
             break;
         case FA2_KERNEL_KEY_SPLIT_64:
             err = causal ? launch_splitk<true, 4, 2>(query, key, value, output, batch_heads, seq_len, scale_log2, s)

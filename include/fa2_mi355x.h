@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define FA2_MI355X_ABI_VERSION 6
+#define FA2_MI355X_ABI_VERSION 7
 
 enum fa2_status {
     FA2_STATUS_SUCCESS = 0,
@@ -48,7 +48,7 @@ enum fa2_status {
  * before the P.V product. The softmax denominator differs from the reference's FP32
  * sum of unrounded probabilities in most kernels: they add the FP16-rounded P in
  * pairs (an FP16 add) and accumulate the pair sums into FP32 with v_dot2, so that
- * O is a convex combination of the P the product used. The causal kernel for 1024
+ * O is a convex combination of the P the product used. The causal kernel for 512
  * to 2047 keys on few heads (FA2_KERNEL_KEY_SPLIT_PAIRS16) sums unrounded FP32 P.
  * Outputs stay within atol 2e-3 + rtol 1e-2 of the FP32 formula.
  * NaN and +-inf inputs make NaN or inf exactly the outputs the FP32 formula does,
@@ -143,8 +143,11 @@ enum fa2_forward_kernel {
     FA2_KERNEL_KEY_SPLIT_8_WAVES = 6, /* keys split over 8 waves, 32-key tiles             */
     FA2_KERNEL_KEY_SPLIT_PAIRS16 = 7, /* causal: 16-query blocks p and N/16-1-p of a head  */
                                       /* per workgroup, keys split over 4 waves            */
-    FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES = 8 /* as KEY_SPLIT_64, plus 4 waves that only fetch */
-                                          /* K/V tiles into LDS for the 4 computing waves  */
+    FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES = 8, /* as KEY_SPLIT_64, plus 4 waves that only fetch */
+                                           /* K/V tiles into LDS for the 4 computing waves  */
+    FA2_KERNEL_128_QUERY_SPLIT_PAIRS = 9   /* causal: 128-query tiles T-1-p and p of a head */
+                                           /* per 8-wave workgroup, keys split between two  */
+                                           /* groups of 4 waves                             */
 };
 
 /*

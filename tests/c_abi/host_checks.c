@@ -122,7 +122,7 @@ int main(void) {
                 for (int causal = 0; causal <= 1; ++causal) {
                     const int64_t batch = counts[a], heads = counts[b], n = sizes[c];
                     const int plan = fa2_forward_plan(batch, heads, n, causal);
-                    CHECK(plan >= FA2_KERNEL_NONE && plan <= FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES, "plan %d", plan);
+                    CHECK(plan >= FA2_KERNEL_NONE && plan <= FA2_KERNEL_128_QUERY_SPLIT_PAIRS, "plan %d", plan);
                     int none = batch <= 0 || heads <= 0 || n <= 0 || n > ((int64_t)1 << 24);
                     if (!none) none = batch > (int64_t)UINT32_MAX / heads;
                     if (!none) none = batch * heads > (int64_t)UINT32_MAX / ((n + 31) / 32);
@@ -176,6 +176,8 @@ int main(void) {
     CHECK(fa2_forward_plan(16, 16, 4096, 0) == FA2_KERNEL_256_QUERY, "plan throughput size");
     CHECK(fa2_forward_plan(16, 16, 4096, 1) == FA2_KERNEL_256_QUERY, "plan throughput size causal");
     CHECK(fa2_forward_plan(16, 16, 1024, 1) == FA2_KERNEL_256_QUERY_PAIRS, "plan causal pairs");
+    CHECK(fa2_forward_plan(1, 8, 8192, 1) == FA2_KERNEL_128_QUERY_SPLIT_PAIRS, "plan split pairs");
+    CHECK(fa2_forward_plan(1, 9, 8192, 1) == FA2_KERNEL_128_QUERY, "plan beyond one round of split pairs");
 
     if (failures) {
         fprintf(stderr, "%d check(s) failed\n", failures);

@@ -39,7 +39,7 @@ def test_status_codes_match_header():
 def test_kernel_ids_match_header():
     text = capi.HEADER_PATH.read_text()
     for name in ("NONE", "256_QUERY", "256_QUERY_PAIRS", "128_QUERY", "KEY_SPLIT_64", "KEY_SPLIT_32",
-                 "KEY_SPLIT_8_WAVES", "KEY_SPLIT_PAIRS16", "KEY_SPLIT_64_DMA_WAVES"):
+                 "KEY_SPLIT_8_WAVES", "KEY_SPLIT_PAIRS16", "KEY_SPLIT_64_DMA_WAVES", "128_QUERY_SPLIT_PAIRS"):
         value = int(re.search(rf"FA2_KERNEL_{name} = (\d+)", text).group(1))
         assert getattr(capi, f"FA2_KERNEL_{name}") == value
 
@@ -70,6 +70,13 @@ K = capi
     (1, 66, 4096, True, K.FA2_KERNEL_256_QUERY), (1, 510, 1024, True, K.FA2_KERNEL_256_QUERY_PAIRS),
     (1, 410, 1280, True, K.FA2_KERNEL_256_QUERY), (1, 409, 1280, True, K.FA2_KERNEL_128_QUERY),
     (1, 64, 1024, True, K.FA2_KERNEL_128_QUERY),
+    # Causal, 320 to 512 groups of 128 with 8192 keys or more (a multiple of 256): pairs
+    # of 128-query tiles split over two wave groups.
+    (1, 8, 8192, True, K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS), (1, 5, 8192, True, K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS),
+    (1, 3, 16384, True, K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS), (2, 4, 8192, True, K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS),
+    (1, 2, 32768, True, K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS), (1, 9, 8192, True, K.FA2_KERNEL_128_QUERY),
+    (1, 16, 4096, True, K.FA2_KERNEL_128_QUERY), (1, 5, 8320, True, K.FA2_KERNEL_128_QUERY),
+    (1, 4, 8192, True, K.FA2_KERNEL_KEY_SPLIT_32), (1, 8, 8192, False, K.FA2_KERNEL_128_QUERY),
     # 128-query from 320 groups of 128.
     (1, 40, 1024, True, K.FA2_KERNEL_128_QUERY), (1, 72, 512, True, K.FA2_KERNEL_KEY_SPLIT_32),
     (1, 57, 1024, True, K.FA2_KERNEL_128_QUERY), (1, 39, 1024, True, K.FA2_KERNEL_KEY_SPLIT_32),

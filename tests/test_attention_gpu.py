@@ -353,6 +353,31 @@ def test_wide_workgroup_shapes_match_oracle(causal, shape, kernel, ramp):
     _assert_close_to_oracle(actual, expected)
 
 
+@pytest.mark.parametrize("ramp", [False, True])
+@pytest.mark.parametrize("shape, sigma", [((1, 8, 8192), 1.0), ((1, 5, 8192), 1.0), ((1, 3, 16384), 2.0)])
+def test_split_pairs_shapes_match_oracle(shape, sigma, ramp):
+    # Causal pairs of 128-query tiles (T-1-p, p) per 8-wave workgroup, the pair's key
+    # tiles split between two groups of 4 waves and merged through LDS. Every row of the
+    # first, middle and last head covers every pair of those heads: the middle pair,
+    # whose heavy keys in group 1 lie wholly past the queries of its waves 0-1, and the
+    # light tiles, whose last key tile waves 0-1 skip. 320 groups (B1 H5 N8192) split
+    # heads across the XCD ranges. sigma = 2 gives large logits; the ramp grows the
+    # key norms 5x along the sequence, forcing the exact-max recompute in both groups
+    # before the merge.
+    batch, heads, seq_len = shape
+    assert capi.forward_plan(batch, heads, seq_len, True) == capi.FA2_KERNEL_128_QUERY_SPLIT_PAIRS
+    q, k, v = _inputs(*shape, seed=23, sigma=sigma)
+    if ramp:
+        k = (k.float() * torch.linspace(1.0, 5.0, seq_len).view(1, 1, -1, 1)).half()
+    out = _run(q, k, v, True).cpu()
+    assert torch.isfinite(out).all()
+    whole = sorted({(0, 0), (batch - 1, heads - 1), (batch // 2, heads // 2)})
+    rows = [(b, h, i) for b, h in whole for i in range(seq_len)] + _sample_rows(batch, heads, seq_len, 64, seed=24)
+    expected = attention_rows_fp32(q, k, v, rows, causal=True)
+    actual = torch.stack([out[b, h, i] for b, h, i in rows])
+    _assert_close_to_oracle(actual, expected)
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_constant_value_gives_constant_output(causal):
     q, k, _ = _inputs(2, 4, 512, seed=5)

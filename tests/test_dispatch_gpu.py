@@ -6,8 +6,10 @@ ends in a partial round that the 128-query kernel's finer rounds finish sooner; 
 one query tile per workgroup in level order (per-XCD head groups when batch*heads is a
 multiple of 8) when a head has at least 8 tiles or the grid 2048; else pairs of query
 tiles when a head has an even number of them, one tile per workgroup from 2048 when odd),
-the 128-query kernel from 256 (noncausal) or 320 (causal) groups of 128 queries, and
-otherwise the key-split kernel: up to 256 query blocks of 32, 4 waves with 64-key tiles
+causal problems of 320 to 512 groups of 128 queries with at least 8192 keys (a multiple of
+256) in pairs of 128-query tiles whose keys two wave groups split, the 128-query kernel
+from 256 (noncausal) or 320 (causal) groups of 128 queries, and otherwise the key-split
+kernel: up to 256 query blocks of 32, 4 waves with 64-key tiles
 (noncausal from 1024 keys with dedicated DMA waves; causal from 512 to 2047 keys, pairs of
 16-query blocks; 8 waves with 32-key tiles from 2048 keys on; 32-key tiles when 64-key
 tiles would split unevenly over the waves, and causal below 512 keys), and 32-key tiles
@@ -75,6 +77,15 @@ CASES = [
     (32, 16, 1024, True, "256-query, head groups (2048 tiles of T = 4)", K.FA2_KERNEL_256_QUERY),
     (1, 64, 4096, True, "256-query, head groups (1024 tiles of T = 16)", K.FA2_KERNEL_256_QUERY),
     (1, 66, 4096, True, "256-query, single tiles (XCD ranges splitting heads)", K.FA2_KERNEL_256_QUERY),
+    (1, 8, 8192, True, "128-query tile pairs split over two wave groups (512 groups of 128)",
+     K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS),
+    (1, 5, 8192, True, "128-query tile pairs split over two wave groups (320 groups, the fewest)",
+     K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS),
+    (1, 3, 16384, True, "128-query tile pairs split over two wave groups (16384 keys)",
+     K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS),
+    (1, 9, 8192, True, "128-query (576 groups of 128, beyond one round)", K.FA2_KERNEL_128_QUERY),
+    (1, 16, 4096, True, "128-query (512 groups of 128, below 8192 keys)", K.FA2_KERNEL_128_QUERY),
+    (1, 5, 8320, True, "128-query (325 groups, an odd number of 128-query tiles per head)", K.FA2_KERNEL_128_QUERY),
 ]
 
 

@@ -2469,8 +2469,9 @@ bool use_128_query_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
 // 128-query kernel (same process, graph replays): -6% to -10% at 8192 keys (B1 H5-H8),
 // -13% to -16% at 16384 (B1 H3-H4, also with sigma = 2 logits), -16% at B1 H2 N32768;
 // -4.5% to +1% at 4096 keys (B1 H10-H16, B2 H8) and 1-14% slower at 256-2048 keys,
-// where its steps, without the 128-query kernel's overlap of one tile's score MFMAs
-// with the previous tile's softmax, cost more than the balance saves.
+// where its steps and fixed costs (Q, the first tiles, the light tile's store, the
+// merge) outweigh the balance. Each wave running the 128-query kernel's software
+// pipeline instead measured 4-30% slower at every length.
 constexpr int64_t kSplitPairsMinKeys = 8192;
 bool use_split_pairs_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
     if (!causal || seq_len % 256 != 0 || seq_len < kSplitPairsMinKeys) return false;

@@ -111,7 +111,29 @@ def _random_shapes(per_route, seed):
     return [shape for route in sorted(picked) for shape in picked[route]]
 
 
-RANDOM_SHAPES = _random_shapes(3, seed=2024)
+def _random_long_shapes(per_route, seed):
+    # The same over long sequences: seq_len a multiple of 256 from 4096 to 16384, causal or
+    # not, batch*heads up to the same work cap (576 heads of 1024 keys), so that the
+    # routes only long key streams reach (the causal split pairs, 8-wave key-split) are
+    # drawn too.
+    gen = torch.Generator().manual_seed(seed)
+    picked = {}
+    for _ in range(20000):
+        seq_len = 256 * int(torch.randint(16, 65, (1,), generator=gen))
+        limit = max(1, (576 * 1024) // seq_len)
+        batch = int(torch.randint(1, 3, (1,), generator=gen))
+        heads = max(1, round(math.exp(float(torch.rand(1, generator=gen)) * math.log(max(1, limit // batch)))))
+        causal = bool(torch.randint(0, 2, (1,), generator=gen))
+        if batch * heads * seq_len > 576 * 1024:
+            continue
+        route = (capi.forward_plan(batch, heads, seq_len, causal), causal)
+        shapes = picked.setdefault(route, [])
+        if len(shapes) < per_route:
+            shapes.append((batch, heads, seq_len, causal))
+    return [shape for route in sorted(picked) for shape in picked[route]]
+
+
+RANDOM_SHAPES = _random_shapes(3, seed=2024) + _random_long_shapes(2, seed=2025)
 
 
 def _inputs(batch, heads, seq_len, seed):

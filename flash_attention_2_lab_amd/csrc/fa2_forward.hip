@@ -1640,6 +1640,81 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_pairs16_kernel(const 
 // group ran between 4% faster and 1% slower than 64 / T on two boxes (B16 H16 N4096, B2 H16
 // N8192, B4 H16 N2048, B2 H32 N16384, B64 H16 N512), and 256 / T up to 2% slower.
 
+// Softmax helpers of the kernels that hold one 32-query block's 64-key tile of scores as two
+// 32x32 accumulators s[0], s[1] (S^T: the lane's query column; register i of key block kb
+// holds key 64t + 32kb + 16(i/8) + 8*half + i%8).
+// Exact tile max and lazy rescale of l and O (bound 2^kRescaleLog2); returns whether the
+// max moved.
+__device__ __forceinline__ bool block_exact_max_update(const f32x16 (&s)[2], float scale_log2, float& m_run,
+                                                       float& l_run, f32x16 (&o)[2]) {
+    float tile_max = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) tile_max = fmaxf(fmaxf(tile_max, s[b][i]), s[b][i + 1]);
+    tile_max = max_across_halves(tile_max);
+    const bool grow = tile_max * scale_log2 > m_run * scale_log2 + kRescaleLog2;
+    if (__builtin_amdgcn_ballot_w64(grow) == 0) return false;
+    const float m_new = fmaxf(m_run, tile_max);
+    const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
+    l_run *= alpha;
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[d][i] *= alpha;
+    m_run = m_new;
+    return true;
+}
+
+// FP16 probabilities of the block against its running max, as P.V B operands
+// (pf[key block][16-key half]); returns the lane sum (pairs added in FP16, then v_dot2
+// against 1.0 into FP32).
+__device__ __forceinline__ float block_tile_probs(const f32x16 (&s)[2], float m_run, float scale_log2,
+                                                  f16x8 (&pf)[2][2]) {
+    const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+    const float m_scaled = m_run * scale_log2;
+    float sum = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        f16x2 pk[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            pk[q] = pack_rn(__builtin_amdgcn_exp2f(fmaf(s[b][2 * q], scale_log2, -m_scaled)),
+                            __builtin_amdgcn_exp2f(fmaf(s[b][2 * q + 1], scale_log2, -m_scaled)));
+            if (q & 1) sum = __builtin_amdgcn_fdot2(pk[q - 1] + pk[q], ones, sum, false);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const f16x4 lo = __builtin_shufflevector(pk[4 * h], pk[4 * h + 1], 0, 1, 2, 3);
+            const f16x4 hi = __builtin_shufflevector(pk[4 * h + 2], pk[4 * h + 3], 0, 1, 2, 3);
+            pf[b][h] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+    }
+    return sum;
+}
+
+// Scores of key tile t past the lane's `query` set to -inf. The sign of limit - offset
+// selects -inf by bit select: compares would be hoisted out of the key loop as 64 lane
+// masks in SGPRs, and spill. Per 8-key group one opaque base, so that every other constant
+// is an inline operand (0..7) rather than an SGPR.
+__device__ __forceinline__ void block_mask_diagonal(f32x16 (&s)[2], int query, int t, int half) {
+    const int limit = query - t * kKeysPerTile - 8 * half;
+    constexpr uint32_t kNegInf = 0xff800000u;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int hi = 0; hi < 2; ++hi) {
+            int base = limit - (32 * kb + 16 * hi);
+            asm volatile("" : "+v"(base));
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = 8 * hi + j;
+                const uint32_t mask = (uint32_t)((base - j) >> 31);
+                s[kb][i] = __uint_as_float((mask & kNegInf) | (~mask & __float_as_uint(s[kb][i])));
+            }
+        }
+}
+
 template <bool kCausal, bool kPairs>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
@@ -1712,53 +1787,7 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
             v_off[r][dblk] = row * kRowBytes + ((chunk ^ tile_swizzle(row)) << 4) + 8 * (i16 & 1);
         }
 
-    const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
 
-    // Exact tile max of one block and lazy rescale of its l and O (bound
-    // 2^kRescaleLog2); returns whether the max moved.
-    auto exact_max_update = [&](const f32x16 (&s)[2], float& m_run, float& l_run, f32x16 (&o)[2]) -> bool {
-        float tile_max = -INFINITY;
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int i = 0; i < 16; i += 2) tile_max = fmaxf(fmaxf(tile_max, s[b][i]), s[b][i + 1]);
-        tile_max = max_across_halves(tile_max);
-        const bool grow = tile_max * scale_log2 > m_run * scale_log2 + kRescaleLog2;
-        if (__builtin_amdgcn_ballot_w64(grow) == 0) return false;
-        const float m_new = fmaxf(m_run, tile_max);
-        const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
-        l_run *= alpha;
-#pragma unroll
-        for (int d = 0; d < 2; ++d)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) o[d][i] *= alpha;
-        m_run = m_new;
-        return true;
-    };
-    // FP16 probabilities of one block against its running max, as P.V B operands
-    // (pf[key block][16-key half]); returns the lane sum (pairs added in FP16, then
-    // v_dot2 against 1.0 into FP32).
-    auto tile_probs = [&](const f32x16 (&s)[2], float m_run, f16x8 (&pf)[2][2]) -> float {
-        const float m_scaled = m_run * scale_log2;
-        float sum = 0.0f;
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            f16x2 pk[8];
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                pk[q] = pack_rn(__builtin_amdgcn_exp2f(fmaf(s[b][2 * q], scale_log2, -m_scaled)),
-                                __builtin_amdgcn_exp2f(fmaf(s[b][2 * q + 1], scale_log2, -m_scaled)));
-                if (q & 1) sum = __builtin_amdgcn_fdot2(pk[q - 1] + pk[q], ones, sum, false);
-            }
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const f16x4 lo = __builtin_shufflevector(pk[4 * h], pk[4 * h + 1], 0, 1, 2, 3);
-                const f16x4 hi = __builtin_shufflevector(pk[4 * h + 2], pk[4 * h + 3], 0, 1, 2, 3);
-                pf[b][h] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-            }
-        }
-        return sum;
-    };
 
     // Epilogue of a pass: O = O^T / l. Accumulator i of d-block dblk holds dim
     // 32*dblk + 8*(i/4) + 4*half + i%4 of the lane's query.
@@ -1839,28 +1868,6 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) asm volatile("" ::"v"(qa[ks]), "v"(qb[ks]));
 
-        // Scores of one block past the diagonal set to -inf: register i of key block kb
-        // holds key 64t + 32kb + 16(i/8) + 8*half + i%8. The sign of limit - offset
-        // selects -inf by bit select: compares would be hoisted out of the loop as 64
-        // lane masks in SGPRs, and spill. Per 8-key group one opaque base, so that every
-        // other constant is an inline operand (0..7) rather than an SGPR.
-        auto mask_diagonal = [&](f32x16 (&s)[2], int query, int t) {
-            const int limit = query - t * kKeysPerTile - 8 * half;
-            constexpr uint32_t kNegInf = 0xff800000u;
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int hi = 0; hi < 2; ++hi) {
-                    int base = limit - (32 * kb + 16 * hi);
-                    asm volatile("" : "+v"(base));
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const int i = 8 * hi + j;
-                        const uint32_t mask = (uint32_t)((base - j) >> 31);
-                        s[kb][i] = __uint_as_float((mask & kNegInf) | (~mask & __float_as_uint(s[kb][i])));
-                    }
-                }
-        };
 
         // One key tile: fetch three ahead, and after the work, wait for tile t+1 (only the
         // fetches of the tiles after it may stay in flight) at a barrier, after which
@@ -1913,23 +1920,23 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
 
             // Causal: block a's diagonal tile. Block b (later queries) sees every key
             // of it.
-            if (kCausal && t == last_a) mask_diagonal(sa, query_a, t);
+            if (kCausal && t == last_a) block_mask_diagonal(sa, query_a, t, half);
 
             // Online softmax per block: exact max on the first tile, then the running
             // max with the lane-sum check (every probability is <= 2^kRescaleLog2 when its lane's
             // sum is), recomputing only a block whose check fails.
             f16x8 pa[2][2], pb[2][2];
             if (t == 0) {
-                exact_max_update(sa, m_a, l_a, oa);
-                exact_max_update(sb, m_b, l_b, ob);
+                block_exact_max_update(sa, scale_log2, m_a, l_a, oa);
+                block_exact_max_update(sb, scale_log2, m_b, l_b, ob);
             }
-            float sum_a = tile_probs(sa, m_a, pa);
-            float sum_b = tile_probs(sb, m_b, pb);
+            float sum_a = block_tile_probs(sa, m_a, scale_log2, pa);
+            float sum_b = block_tile_probs(sb, m_b, scale_log2, pb);
             if (t != 0) {
-                if (__builtin_amdgcn_ballot_w64(sum_a > kTileSumBound) != 0 && exact_max_update(sa, m_a, l_a, oa))
-                    sum_a = tile_probs(sa, m_a, pa);
-                if (__builtin_amdgcn_ballot_w64(sum_b > kTileSumBound) != 0 && exact_max_update(sb, m_b, l_b, ob))
-                    sum_b = tile_probs(sb, m_b, pb);
+                if (__builtin_amdgcn_ballot_w64(sum_a > kTileSumBound) != 0 && block_exact_max_update(sa, scale_log2, m_a, l_a, oa))
+                    sum_a = block_tile_probs(sa, m_a, scale_log2, pa);
+                if (__builtin_amdgcn_ballot_w64(sum_b > kTileSumBound) != 0 && block_exact_max_update(sb, scale_log2, m_b, l_b, ob))
+                    sum_b = block_tile_probs(sb, m_b, scale_log2, pb);
             }
             l_a += sum_a;
             l_b += sum_b;
@@ -1977,11 +1984,11 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
                     const f16x4 v_hi = lds_read_transposed(v_lds + row_base + v_off[1][k & 1]);
                     vf[k] = __builtin_shufflevector(v_lo, v_hi, 0, 1, 2, 3, 4, 5, 6, 7);
                 }
-                if (t == last_b) mask_diagonal(sb, query_b, t);
+                if (t == last_b) block_mask_diagonal(sb, query_b, t, half);
                 f16x8 pb[2][2];
-                float sum_b = tile_probs(sb, m_b, pb);
-                if (__builtin_amdgcn_ballot_w64(sum_b > kTileSumBound) != 0 && exact_max_update(sb, m_b, l_b, ob))
-                    sum_b = tile_probs(sb, m_b, pb);
+                float sum_b = block_tile_probs(sb, m_b, scale_log2, pb);
+                if (__builtin_amdgcn_ballot_w64(sum_b > kTileSumBound) != 0 && block_exact_max_update(sb, scale_log2, m_b, l_b, ob))
+                    sum_b = block_tile_probs(sb, m_b, scale_log2, pb);
                 l_b += sum_b;
                 __builtin_amdgcn_sched_barrier(0);
                 __builtin_amdgcn_s_setprio(1);
@@ -2095,7 +2102,6 @@ void fa2_forward_d64_split_pairs_kernel(const _Float16* __restrict__ query,
             const int chunk = 4 * dblk + 2 * (grp & 1) + ((i16 & 3) >> 1);
             v_off[r][dblk] = row * kRowBytes + ((chunk ^ tile_swizzle(row)) << 4) + 8 * (i16 & 1);
         }
-    const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
 
     // First query of this wave's 32-query block in each tile.
     const int q_heavy = heavy * 128 + gw * kQueriesPerWave;
@@ -2114,69 +2120,6 @@ void fa2_forward_d64_split_pairs_kernel(const _Float16* __restrict__ query,
     dma_step(1);
     dma_step(2);  // steps = T + 1 >= 3
 
-    // Exact tile max and lazy rescale of l and O (bound 2^kRescaleLog2); returns
-    // whether the max moved.
-    auto exact_max_update = [&](const f32x16 (&s)[2], float& m_run, float& l_run, f32x16 (&o)[2]) -> bool {
-        float tile_max = -INFINITY;
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int i = 0; i < 16; i += 2) tile_max = fmaxf(fmaxf(tile_max, s[b][i]), s[b][i + 1]);
-        tile_max = max_across_halves(tile_max);
-        const bool grow = tile_max * scale_log2 > m_run * scale_log2 + kRescaleLog2;
-        if (__builtin_amdgcn_ballot_w64(grow) == 0) return false;
-        const float m_new = fmaxf(m_run, tile_max);
-        const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
-        l_run *= alpha;
-#pragma unroll
-        for (int d = 0; d < 2; ++d)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) o[d][i] *= alpha;
-        m_run = m_new;
-        return true;
-    };
-    // FP16 probabilities against the running max as P.V B operands; returns the lane
-    // sum (pairs added in FP16, then v_dot2 against 1.0 into FP32).
-    auto tile_probs = [&](const f32x16 (&s)[2], float m_run, f16x8 (&pf)[2][2]) -> float {
-        const float m_scaled = m_run * scale_log2;
-        float sum = 0.0f;
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            f16x2 pk[8];
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                pk[q] = pack_rn(__builtin_amdgcn_exp2f(fmaf(s[b][2 * q], scale_log2, -m_scaled)),
-                                __builtin_amdgcn_exp2f(fmaf(s[b][2 * q + 1], scale_log2, -m_scaled)));
-                if (q & 1) sum = __builtin_amdgcn_fdot2(pk[q - 1] + pk[q], ones, sum, false);
-            }
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const f16x4 lo = __builtin_shufflevector(pk[4 * h], pk[4 * h + 1], 0, 1, 2, 3);
-                const f16x4 hi = __builtin_shufflevector(pk[4 * h + 2], pk[4 * h + 3], 0, 1, 2, 3);
-                pf[b][h] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-            }
-        }
-        return sum;
-    };
-    // Scores past the diagonal set to -inf (register i of key block kb holds key
-    // 64t + 32kb + 16(i/8) + 8*half + i%8), by bit select on the sign of limit - offset.
-    auto mask_diagonal = [&](f32x16 (&s)[2], int query, int t) {
-        const int limit = query - t * kKeysPerTile - 8 * half;
-        constexpr uint32_t kNegInf = 0xff800000u;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int hi = 0; hi < 2; ++hi) {
-                int base = limit - (32 * kb + 16 * hi);
-                asm volatile("" : "+v"(base));
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int i = 8 * hi + j;
-                    const uint32_t mask = (uint32_t)((base - j) >> 31);
-                    s[kb][i] = __uint_as_float((mask & kNegInf) | (~mask & __float_as_uint(s[kb][i])));
-                }
-            }
-    };
     // O / l of one 32-query block as FP16: accumulator i of d-block dblk holds dim
     // 32*dblk + 8*(i/4) + 4*half + i%4 of the lane's query; 8-byte stores.
     auto store_block = [&](const f32x16 (&o)[2], float l_lane, int q_first) {
@@ -2251,14 +2194,14 @@ void fa2_forward_d64_split_pairs_kernel(const _Float16* __restrict__ query,
                 const f16x4 v_hi = lds_read_transposed(v_lds + row_base + v_off[1][k & 1]);
                 vf[k] = __builtin_shufflevector(v_lo, v_hi, 0, 1, 2, 3, 4, 5, 6, 7);
             }
-            if (kt * kKeysPerTile + kKeysPerTile - 1 > q_first) mask_diagonal(sc, q_first + lq, kt);
+            if (kt * kKeysPerTile + kKeysPerTile - 1 > q_first) block_mask_diagonal(sc, q_first + lq, kt, half);
             const bool first = fresh;
             fresh = false;
-            if (first) exact_max_update(sc, m_run, l_run, o);
+            if (first) block_exact_max_update(sc, scale_log2, m_run, l_run, o);
             f16x8 pf[2][2];
-            float sum = tile_probs(sc, m_run, pf);
-            if (!first && __builtin_amdgcn_ballot_w64(sum > kTileSumBound) != 0 && exact_max_update(sc, m_run, l_run, o))
-                sum = tile_probs(sc, m_run, pf);
+            float sum = block_tile_probs(sc, m_run, scale_log2, pf);
+            if (!first && __builtin_amdgcn_ballot_w64(sum > kTileSumBound) != 0 && block_exact_max_update(sc, scale_log2, m_run, l_run, o))
+                sum = block_tile_probs(sc, m_run, scale_log2, pf);
             l_run += sum;
             __builtin_amdgcn_sched_barrier(0);
             __builtin_amdgcn_s_setprio(1);

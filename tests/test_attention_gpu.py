@@ -412,15 +412,16 @@ def test_runs_on_the_current_stream():
 
 def test_concurrent_streams_do_not_interfere():
     # The forward keeps no state between calls (no scratch memory, no counters), so
-    # calls on different streams may overlap. Two side streams each run ten forwards
-    # of their own shape and inputs (256-query kernel, causal pairs; key-split kernel)
-    # at the same time; every output must equal the sequential result bitwise.
-    cases = [((8, 64, 1024), True, 51), ((1, 8, 1024), False, 52)]
+    # calls on different streams may overlap. Three side streams each run ten forwards
+    # of their own shape and inputs (256-query kernel, causal pairs; key-split kernel;
+    # causal split pairs, 128 KiB of LDS per workgroup) at the same time; every output
+    # must equal the sequential result bitwise.
+    cases = [((8, 64, 1024), True, 51), ((1, 8, 1024), False, 52), ((1, 5, 8192), True, 53)]
     inputs = [[t.cuda() for t in _inputs(*shape, seed=seed)] for shape, _, seed in cases]
     expected = [ENTRY(*x, causal) for x, (_, causal, _) in zip(inputs, cases)]
     torch.cuda.synchronize()
     streams = [torch.cuda.Stream() for _ in cases]
-    outputs = [[], []]
+    outputs = [[] for _ in cases]
     for s in streams:
         s.wait_stream(torch.cuda.current_stream())
     for _ in range(10):
@@ -434,13 +435,15 @@ def test_concurrent_streams_do_not_interfere():
 
 
 @pytest.mark.parametrize("shape, causal", [((1, 8, 1024), False), ((1, 8, 1024), True),
-                                           ((8, 16, 1024), False), ((8, 64, 1024), True)])
+                                           ((8, 16, 1024), False), ((8, 64, 1024), True),
+                                           ((1, 5, 8192), True)])
 def test_forward_replays_in_a_hip_graph(shape, causal):
     # The forward launches one kernel on the current stream and allocates nothing but
     # its output, so it can be captured in a HIP graph (the bench size is bound by
     # launch overhead). Each replay gets new inputs copied into the captured buffers,
     # with eager work and a synchronization in between, and must equal the eager call
-    # bitwise. Shapes: key-split kernel (B1 H8 N1024) and the 256-query kernel.
+    # bitwise. Shapes: key-split kernels (B1 H8 N1024), the 256-query kernel and the
+    # causal split pairs (B1 H5 N8192).
     static = [t.cuda() for t in _inputs(*shape, seed=21)]
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())

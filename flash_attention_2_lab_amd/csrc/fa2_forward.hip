@@ -2414,7 +2414,9 @@ bool use_128_query_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
 // -4.5% to +1% at 4096 keys (B1 H10-H16, B2 H8) and 1-14% slower at 256-2048 keys,
 // where its steps and fixed costs (Q, the first tiles, the light tile's store, the
 // merge) outweigh the balance. Each wave running the 128-query kernel's software
-// pipeline instead measured 4-30% slower at every length.
+// pipeline instead measured 4-30% slower at every length. Beyond 512 groups the
+// 128-query kernel's level order balances its rounds, and the split pairs (several
+// rounds of one workgroup per CU) ran 20-45% slower (B1 H10-H16 N8192, B1 H5-H8 N16384).
 constexpr int64_t kSplitPairsMinKeys = 8192;
 bool use_split_pairs_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
     if (!causal || seq_len % 256 != 0 || seq_len < kSplitPairsMinKeys) return false;

@@ -6,8 +6,8 @@
  * noncausal O[i] = mean over all keys of V, causal O[i] = mean of V[0..i]. Those are
  * computed on the host in double and compared with the FP16 output (atol 2e-3 + rtol
  * 1e-2). V[j][d] = ((j * 37 + d * 11) % 101) / 50 - 1 is exact in FP16. Also checks
- * argument rejection, the empty problem and fa2_forward_plan. Prints "ok" and exits 0
- * when every check passes.
+ * argument rejection, the empty problem and fa2_forward_plan, and the causal closed form at
+ * a size the split pairs run (B1 H5 N8192). Prints "ok" and exits 0 when every check passes.
  */
 #include <math.h>
 #include <stdint.h>
@@ -67,6 +67,61 @@ static float from_half(uint16_t h) {
 }
 
 static double v_value(int j, int d) { return (double)((j * 37 + d * 11) % 101) / 50.0 - 1.0; }
+
+/* Causal, Q = K = 0, at a size the causal split pairs run (batch*heads*seq_len/128 = 320,
+ * seq_len 8192): O[i] is the mean of V[0..i], from prefix sums. Returns 0 on success. */
+static int check_causal_prefix_means(int64_t batch, int64_t heads, int64_t seq_len) {
+    const size_t elems = (size_t)(batch * heads * seq_len) * D;
+    const size_t bytes = elems * sizeof(uint16_t);
+    uint16_t* host_zero = calloc(elems, sizeof(uint16_t));
+    uint16_t* host_v = malloc(bytes);
+    uint16_t* host_o = malloc(bytes);
+    double* prefix = malloc(sizeof(double) * D);
+    if (!host_zero || !host_v || !host_o || !prefix) return 2;
+    for (int64_t bh = 0; bh < batch * heads; ++bh)
+        for (int64_t j = 0; j < seq_len; ++j)
+            for (int d = 0; d < D; ++d) host_v[((size_t)bh * seq_len + j) * D + d] = to_half((float)v_value((int)j, d));
+    void *q, *k, *v, *o;
+    if (hipMalloc(&q, bytes) != hipSuccess || hipMalloc(&k, bytes) != hipSuccess ||
+        hipMalloc(&v, bytes) != hipSuccess || hipMalloc(&o, bytes) != hipSuccess)
+        return 2;
+    hipMemcpy(q, host_zero, bytes, hipMemcpyHostToDevice);
+    hipMemcpy(k, host_zero, bytes, hipMemcpyHostToDevice);
+    hipMemcpy(v, host_v, bytes, hipMemcpyHostToDevice);
+    hipMemset(o, 0xff, bytes); /* NaN pattern: every output must be written */
+    const int status = fa2_forward_production_128x128(q, k, v, o, batch, heads, seq_len, D, 1, NULL);
+    CHECK(status == FA2_STATUS_SUCCESS, "split pairs: status %d (%s)", status, fa2_status_string(status));
+    if (hipDeviceSynchronize() != hipSuccess) return 2;
+    hipMemcpy(host_o, o, bytes, hipMemcpyDeviceToHost);
+    double worst = 0.0;
+    for (int64_t bh = 0; bh < batch * heads; ++bh) {
+        for (int d = 0; d < D; ++d) prefix[d] = 0.0;
+        for (int64_t i = 0; i < seq_len; ++i)
+            for (int d = 0; d < D; ++d) {
+                prefix[d] += v_value((int)i, d);
+                const double mean = prefix[d] / (double)(i + 1);
+                const double got = from_half(host_o[((size_t)bh * seq_len + i) * D + d]);
+                if (!(fabs(got - mean) - (2e-3 + 1e-2 * fabs(mean)) <= 0.0)) {
+                    ++failures;
+                    if (failures < 5)
+                        fprintf(stderr, "split pairs bh=%lld i=%lld d=%d: got %f want %f\n", (long long)bh,
+                                (long long)i, d, got, mean);
+                }
+                if (fabs(got - mean) > worst) worst = fabs(got - mean);
+            }
+    }
+    printf("split pairs (B%lld H%lld N%lld causal): max abs error %.3e\n", (long long)batch, (long long)heads,
+           (long long)seq_len, worst);
+    hipFree(q);
+    hipFree(k);
+    hipFree(v);
+    hipFree(o);
+    free(host_zero);
+    free(host_v);
+    free(host_o);
+    free(prefix);
+    return 0;
+}
 
 int main(void) {
     const size_t elems = (size_t)B * H * N * D;
@@ -131,6 +186,12 @@ int main(void) {
     CHECK(fa2_forward_plan(16, 16, 4096, 1) == FA2_KERNEL_256_QUERY, "plan big causal");
     CHECK(fa2_forward_plan(16, 16, 1024, 1) == FA2_KERNEL_256_QUERY_PAIRS, "plan causal pairs");
     CHECK(strcmp(fa2_status_string(FA2_STATUS_BAD_HEAD_DIM), "head dimension must equal 64") == 0, "status text");
+
+    CHECK(fa2_forward_plan(1, 5, 8192, 1) == FA2_KERNEL_128_QUERY_SPLIT_PAIRS, "plan split pairs");
+    if (check_causal_prefix_means(1, 5, 8192) != 0) {
+        fprintf(stderr, "split pairs check could not run\n");
+        return 2;
+    }
 
     hipFree(q);
     hipFree(k);

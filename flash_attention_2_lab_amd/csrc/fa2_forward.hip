@@ -1642,45 +1642,47 @@ __global__ __launch_bounds__(kSplit * 64) void fa2_forward_pairs16_kernel(const 
 
 // Softmax helpers of the kernels that hold one 32-query block's 64-key tile of scores as two
 // 32x32 accumulators s[0], s[1] (S^T: the lane's query column; register i of key block kb
-// holds key 64t + 32kb + 16(i/8) + 8*half + i%8).
+// holds key 64t + 32kb + 16(i/8) + 8*half + i%8). The running max is kept scaled,
+// mc = max * scale_log2 (log2 units), so a probability is exp2(s * scale_log2 - mc): one FMA,
+// with no per-tile product of the max.
 // Exact tile max and lazy rescale of l and O (bound 2^kRescaleLog2); returns whether the
-// max moved.
-__device__ __forceinline__ bool block_exact_max_update(const f32x16 (&s)[2], float scale_log2, float& m_run,
+// max moved. The rescale factor exp2(mc_old - mc_new) is the exact ratio between the
+// probabilities formed against the two maxima.
+__device__ __forceinline__ bool block_exact_max_update(const f32x16 (&s)[2], float scale_log2, float& mc_run,
                                                        float& l_run, f32x16 (&o)[2]) {
     float tile_max = -INFINITY;
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int i = 0; i < 16; i += 2) tile_max = fmaxf(fmaxf(tile_max, s[b][i]), s[b][i + 1]);
-    tile_max = max_across_halves(tile_max);
-    const bool grow = tile_max * scale_log2 > m_run * scale_log2 + kRescaleLog2;
+    const float tile_mc = max_across_halves(tile_max) * scale_log2;
+    const bool grow = tile_mc > mc_run + kRescaleLog2;
     if (__builtin_amdgcn_ballot_w64(grow) == 0) return false;
-    const float m_new = fmaxf(m_run, tile_max);
-    const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
+    const float mc_new = fmaxf(mc_run, tile_mc);
+    const float alpha = __builtin_amdgcn_exp2f(mc_run - mc_new);
     l_run *= alpha;
 #pragma unroll
     for (int d = 0; d < 2; ++d)
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[d][i] *= alpha;
-    m_run = m_new;
+    mc_run = mc_new;
     return true;
 }
 
-// FP16 probabilities of the block against its running max, as P.V B operands
+// FP16 probabilities of the block against its scaled running max, as P.V B operands
 // (pf[key block][16-key half]); returns the lane sum (pairs added in FP16, then v_dot2
 // against 1.0 into FP32).
-__device__ __forceinline__ float block_tile_probs(const f32x16 (&s)[2], float m_run, float scale_log2,
+__device__ __forceinline__ float block_tile_probs(const f32x16 (&s)[2], float mc_run, float scale_log2,
                                                   f16x8 (&pf)[2][2]) {
     const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
-    const float m_scaled = m_run * scale_log2;
     float sum = 0.0f;
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
         f16x2 pk[8];
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-            pk[q] = pack_rn(__builtin_amdgcn_exp2f(fmaf(s[b][2 * q], scale_log2, -m_scaled)),
-                            __builtin_amdgcn_exp2f(fmaf(s[b][2 * q + 1], scale_log2, -m_scaled)));
+            pk[q] = pack_rn(__builtin_amdgcn_exp2f(fmaf(s[b][2 * q], scale_log2, -mc_run)),
+                            __builtin_amdgcn_exp2f(fmaf(s[b][2 * q + 1], scale_log2, -mc_run)));
             if (q & 1) sum = __builtin_amdgcn_fdot2(pk[q - 1] + pk[q], ones, sum, false);
         }
 #pragma unroll
@@ -1770,11 +1772,27 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
         }
     };
 
+    // LDS addresses of the lane's K fragments in stage 0 (stage s is kStageBytes * s
+    // further; the second 32-key block 4 KiB further). Kept whole in VGPRs, so that a
+    // fragment address is one add of the stage offset per 16-dim step.
     const int k_row = key_of_mfma_row(lq);
     const int k_swz = tile_swizzle(k_row);
-    int k_off[4];
+    uint32_t k_addr[4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) k_off[ks] = k_row * kRowBytes + (((2 * ks + half) ^ k_swz) << 4);
+    for (int ks = 0; ks < 4; ++ks) {
+        k_addr[ks] = smem_addr + (uint32_t)(k_row * kRowBytes + (((2 * ks + half) ^ k_swz) << 4));
+        asm volatile("" : "+v"(k_addr[ks]));
+    }
+    // K fragments of tile t: kf[key block][16-dim step].
+    auto read_k = [&](int t, f16x8 (&kf)[2][4]) {
+        const uint32_t stage_off = (uint32_t)((t & (kStages - 1)) * kStageBytes);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const FA2_LDS f16x8* frag = reinterpret_cast<const FA2_LDS f16x8*>((size_t)(k_addr[ks] + stage_off));
+#pragma unroll
+            for (int b = 0; b < 2; ++b) kf[b][ks] = frag[b * 32 * kRowBytes / 16];
+        }
+    };
     const int grp = lane >> 4;
     const int i16 = lane & 15;
     int v_off[2][2];
@@ -1858,7 +1876,7 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
                 oa[d][i] = 0.0f;
                 ob[d][i] = 0.0f;
             }
-        float m_a = -INFINITY, m_b = -INFINITY;  // running max of raw scores per block
+        float mc_a = -INFINITY, mc_b = -INFINITY;  // running max per block, times scale_log2
         float l_a = 0.0f, l_b = 0.0f;            // this lane's share of each denominator
 
         // Prologue: tiles 0..2 and Q landed. The empty asm consumes Q where the compiler
@@ -1883,19 +1901,17 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
         int t = 0;
         for (; t <= last_a; ++t) {
             fetch_ahead(t);
-            const uint8_t* k_lds = smem + (t & (kStages - 1)) * kStageBytes;
-            const uint8_t* v_lds = k_lds + kTileBytes;
+            const uint8_t* v_lds = smem + (t & (kStages - 1)) * kStageBytes + kTileBytes;
             // S^T = K Q^T of both blocks; each K fragment feeds two MFMAs. The MFMA
             // phases run at raised wave priority: when both waves of a SIMD can
             // issue, the one with MFMAs goes first and the other's softmax fills the
-            // MFMA shadow.
+            // MFMA shadow. All eight K reads are issued before the first MFMA, and all
+            // sixteen V^T reads before the softmax (the scheduling barriers keep the
+            // compiler from spreading them over the phases).
             __builtin_amdgcn_s_setprio(1);
             f16x8 kf[2][4];
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-                for (int b = 0; b < 2; ++b)
-                    kf[b][ks] = *reinterpret_cast<const f16x8*>(k_lds + b * 32 * kRowBytes + k_off[ks]);
+            read_k(t, kf);
+            __builtin_amdgcn_sched_barrier(0);
             f32x16 sa[2], sb[2];
             const f32x16 zero = {};
 #pragma unroll
@@ -1917,6 +1933,7 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
                 const f16x4 v_hi = lds_read_transposed(v_lds + row_base + v_off[1][k & 1]);
                 vf[k] = __builtin_shufflevector(v_lo, v_hi, 0, 1, 2, 3, 4, 5, 6, 7);
             }
+            __builtin_amdgcn_sched_barrier(0);
 
             // Causal: block a's diagonal tile. Block b (later queries) sees every key
             // of it.
@@ -1927,16 +1944,16 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
             // sum is), recomputing only a block whose check fails.
             f16x8 pa[2][2], pb[2][2];
             if (t == 0) {
-                block_exact_max_update(sa, scale_log2, m_a, l_a, oa);
-                block_exact_max_update(sb, scale_log2, m_b, l_b, ob);
+                block_exact_max_update(sa, scale_log2, mc_a, l_a, oa);
+                block_exact_max_update(sb, scale_log2, mc_b, l_b, ob);
             }
-            float sum_a = block_tile_probs(sa, m_a, scale_log2, pa);
-            float sum_b = block_tile_probs(sb, m_b, scale_log2, pb);
+            float sum_a = block_tile_probs(sa, mc_a, scale_log2, pa);
+            float sum_b = block_tile_probs(sb, mc_b, scale_log2, pb);
             if (t != 0) {
-                if (__builtin_amdgcn_ballot_w64(sum_a > kTileSumBound) != 0 && block_exact_max_update(sa, scale_log2, m_a, l_a, oa))
-                    sum_a = block_tile_probs(sa, m_a, scale_log2, pa);
-                if (__builtin_amdgcn_ballot_w64(sum_b > kTileSumBound) != 0 && block_exact_max_update(sb, scale_log2, m_b, l_b, ob))
-                    sum_b = block_tile_probs(sb, m_b, scale_log2, pb);
+                if (__builtin_amdgcn_ballot_w64(sum_a > kTileSumBound) != 0 && block_exact_max_update(sa, scale_log2, mc_a, l_a, oa))
+                    sum_a = block_tile_probs(sa, mc_a, scale_log2, pa);
+                if (__builtin_amdgcn_ballot_w64(sum_b > kTileSumBound) != 0 && block_exact_max_update(sb, scale_log2, mc_b, l_b, ob))
+                    sum_b = block_tile_probs(sb, mc_b, scale_log2, pb);
             }
             l_a += sum_a;
             l_b += sum_b;
@@ -1958,15 +1975,11 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
             // (t >= 1 here, so its running max is set).
             for (; t <= last_b; ++t) {
                 fetch_ahead(t);
-                const uint8_t* k_lds = smem + (t & (kStages - 1)) * kStageBytes;
-                const uint8_t* v_lds = k_lds + kTileBytes;
+                const uint8_t* v_lds = smem + (t & (kStages - 1)) * kStageBytes + kTileBytes;
                 __builtin_amdgcn_s_setprio(1);
                 f16x8 kf[2][4];
-#pragma unroll
-                for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-                    for (int b = 0; b < 2; ++b)
-                        kf[b][ks] = *reinterpret_cast<const f16x8*>(k_lds + b * 32 * kRowBytes + k_off[ks]);
+                read_k(t, kf);
+                __builtin_amdgcn_sched_barrier(0);
                 f32x16 sb[2];
                 const f32x16 zero = {};
 #pragma unroll
@@ -1984,11 +1997,12 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
                     const f16x4 v_hi = lds_read_transposed(v_lds + row_base + v_off[1][k & 1]);
                     vf[k] = __builtin_shufflevector(v_lo, v_hi, 0, 1, 2, 3, 4, 5, 6, 7);
                 }
+                __builtin_amdgcn_sched_barrier(0);
                 if (t == last_b) block_mask_diagonal(sb, query_b, t, half);
                 f16x8 pb[2][2];
-                float sum_b = block_tile_probs(sb, m_b, scale_log2, pb);
-                if (__builtin_amdgcn_ballot_w64(sum_b > kTileSumBound) != 0 && block_exact_max_update(sb, scale_log2, m_b, l_b, ob))
-                    sum_b = block_tile_probs(sb, m_b, scale_log2, pb);
+                float sum_b = block_tile_probs(sb, mc_b, scale_log2, pb);
+                if (__builtin_amdgcn_ballot_w64(sum_b > kTileSumBound) != 0 && block_exact_max_update(sb, scale_log2, mc_b, l_b, ob))
+                    sum_b = block_tile_probs(sb, mc_b, scale_log2, pb);
                 l_b += sum_b;
                 __builtin_amdgcn_sched_barrier(0);
                 __builtin_amdgcn_s_setprio(1);
@@ -2142,7 +2156,7 @@ void fa2_forward_d64_split_pairs_kernel(const _Float16* __restrict__ query,
     for (int d = 0; d < 2; ++d)
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[d][i] = 0.0f;
-    float m_run = -INFINITY;  // running max of raw scores
+    float mc_run = -INFINITY;  // running max of the scores, times scale_log2
     float l_run = 0.0f;       // this lane's share of the denominator
     bool fresh = true;        // no key tile computed yet for the current query tile
 
@@ -2159,7 +2173,7 @@ void fa2_forward_d64_split_pairs_kernel(const _Float16* __restrict__ query,
             for (int d = 0; d < 2; ++d)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) o[d][i] = 0.0f;
-            m_run = -INFINITY;
+            mc_run = -INFINITY;
             l_run = 0.0f;
             fresh = true;
 #pragma unroll
@@ -2197,11 +2211,11 @@ void fa2_forward_d64_split_pairs_kernel(const _Float16* __restrict__ query,
             if (kt * kKeysPerTile + kKeysPerTile - 1 > q_first) block_mask_diagonal(sc, q_first + lq, kt, half);
             const bool first = fresh;
             fresh = false;
-            if (first) block_exact_max_update(sc, scale_log2, m_run, l_run, o);
+            if (first) block_exact_max_update(sc, scale_log2, mc_run, l_run, o);
             f16x8 pf[2][2];
-            float sum = block_tile_probs(sc, m_run, scale_log2, pf);
-            if (!first && __builtin_amdgcn_ballot_w64(sum > kTileSumBound) != 0 && block_exact_max_update(sc, scale_log2, m_run, l_run, o))
-                sum = block_tile_probs(sc, m_run, scale_log2, pf);
+            float sum = block_tile_probs(sc, mc_run, scale_log2, pf);
+            if (!first && __builtin_amdgcn_ballot_w64(sum > kTileSumBound) != 0 && block_exact_max_update(sc, scale_log2, mc_run, l_run, o))
+                sum = block_tile_probs(sc, mc_run, scale_log2, pf);
             l_run += sum;
             __builtin_amdgcn_sched_barrier(0);
             __builtin_amdgcn_s_setprio(1);
@@ -2226,16 +2240,16 @@ void fa2_forward_d64_split_pairs_kernel(const _Float16* __restrict__ query,
         for (int d = 0; d < 2; ++d)
 #pragma unroll
             for (int i = 0; i < 16; ++i) handoff[(16 * d + i) * 64 + lane] = o[d][i];
-        handoff[32 * 64 + lane] = m_run;
+        handoff[32 * 64 + lane] = mc_run;
         handoff[33 * 64 + lane] = l_run;
     }
     __syncthreads();
     if (group == 0) {
-        const float m_other = handoff[32 * 64 + lane];
+        const float mc_other = handoff[32 * 64 + lane];
         const float l_other = handoff[33 * 64 + lane];
-        const float m_new = fmaxf(m_run, m_other);
-        const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * scale_log2);
-        const float alpha_other = __builtin_amdgcn_exp2f((m_other - m_new) * scale_log2);  // 0 when m_other = -inf
+        const float mc_new = fmaxf(mc_run, mc_other);
+        const float alpha = __builtin_amdgcn_exp2f(mc_run - mc_new);
+        const float alpha_other = __builtin_amdgcn_exp2f(mc_other - mc_new);  // 0 when mc_other = -inf
 #pragma unroll
         for (int d = 0; d < 2; ++d)
 #pragma unroll

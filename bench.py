@@ -145,25 +145,44 @@ def time_in_graph(entry, inputs, modes, steps, replays=3):
     return result
 
 
-TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.json")
+REPO = os.path.dirname(os.path.abspath(__file__))
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "hbm_traffic.json")
+# The kernel source the traffic figures were measured on: the committed summary records
+# its SHA-256, and a summary taken on another version of the source is not reported.
+KERNEL_SOURCE = os.path.join(REPO, "flash_attention_2_lab_amd", "csrc", "fa2_forward.hip")
+
+
+def kernel_source_digest():
+    import hashlib
+
+    with open(KERNEL_SOURCE, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()
 
 
 def measured_traffic(key):
-    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
-    (calibrated on a plain copy), or None when that workload was not profiled."""
+    """(HBM bytes per launch, status) from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary (calibrated on a plain copy). Bytes are None, with status "not profiled" or
+    "stale", when that workload was not profiled or the summary was taken on another
+    version of the kernel source."""
     try:
         with open(TRAFFIC_FILE) as f:
-            entry = json.load(f)["kernels"].get(key)
+            summary = json.load(f)
+        entry = summary["kernels"].get(key)
     except (OSError, ValueError, KeyError):
-        return None
-    return None if entry is None else entry["hbm_bytes"]
+        return None, "not profiled"
+    if entry is None:
+        return None, "not profiled"
+    if summary.get("source_sha256") != kernel_source_digest():
+        return None, "stale"
+    return entry["hbm_bytes"], "current"
 
 
 def roofline(flops, avg_s, traffic_key=None):
     achieved = flops / avg_s / 1e12
+    traffic, status = measured_traffic(traffic_key) if traffic_key else (None, "not profiled")
     return {"bound": "mfma", "achieved": round(achieved, 3), "peak": MI355X_FP16_DENSE_TFLOPS,
             "unit": "TFLOP/s", "frac": round(achieved / MI355X_FP16_DENSE_TFLOPS, 5),
-            "traffic": measured_traffic(traffic_key) if traffic_key else None}
+            "traffic": traffic, "traffic_status": status}
 
 
 # Workloads of the benchmark configurations: (batch, heads, seq_len, sigma).
@@ -189,6 +208,67 @@ def traffic_keys():
 # Plain device-to-device copy of a known size: calibrates the FETCH_SIZE and
 # WRITE_SIZE counters (each should read this many bytes per dispatch).
 COPY_CALIBRATION_BYTES = 256 << 20
+COPY_KERNEL = "__amd_rocclr_copyBuffer"
+
+
+def _counter_kib(csv_path, kernel_prefix):
+    """Median per-dispatch value (KiB) of the one counter in a rocprofv3 counter CSV, over
+    the dispatches whose kernel name starts with `kernel_prefix`; also returns the name."""
+    import csv
+
+    values, names = [], set()
+    with open(csv_path, newline="") as f:
+        for row in csv.DictReader(f):
+            if row["Kernel_Name"].startswith(kernel_prefix):
+                values.append(float(row["Counter_Value"]))
+                names.add(row["Kernel_Name"])
+    if not values or len(names) != 1:
+        raise ValueError(f"{csv_path}: expected one kernel named {kernel_prefix}*, found {sorted(names)}")
+    values.sort()
+    return values[len(values) // 2], names.pop()
+
+
+def write_traffic_summary(run_dir):
+    """Builds profiles/hbm_traffic.json from rocprofv3 counter runs under `run_dir`, one
+    counter and one mode per run:
+        rocprofv3 --pmc <C> -f csv -d <run_dir>/<W>_<M>_<C> -o run -- python3 bench.py --only <W> --mode <M>
+    for C in FETCH_SIZE, WRITE_SIZE, each traffic key <W>/<M>, and <W>_<M> = copy_both. Each
+    counter is scaled by what it reads for the plain copy of known size; the summary
+    records the SHA-256 of the kernel source it was measured on."""
+    def csv_of(stem, counter):
+        return os.path.join(run_dir, f"{stem}_{counter}", "run_counter_collection.csv")
+
+    fetch_copy, _ = _counter_kib(csv_of("copy_both", "FETCH_SIZE"), COPY_KERNEL)
+    write_copy, _ = _counter_kib(csv_of("copy_both", "WRITE_SIZE"), COPY_KERNEL)
+    copy_kib = COPY_CALIBRATION_BYTES / 1024
+    fetch_factor, write_factor = copy_kib / fetch_copy, copy_kib / write_copy
+    summary = {"source_sha256": kernel_source_digest(),
+               "calibration": {"kernel": COPY_KERNEL, "bytes": COPY_CALIBRATION_BYTES,
+                               "fetch_kib": round(fetch_copy, 1), "write_kib": round(write_copy, 1),
+                               "fetch_factor": round(fetch_factor, 4), "write_factor": round(write_factor, 4)},
+               "kernels": {}}
+    for key in traffic_keys():
+        workload, mode = key.split("/")
+        batch, heads, seq_len, _ = WORKLOADS[workload]
+        stem = f"{workload}_{mode}"
+        fetch, name = _counter_kib(csv_of(stem, "FETCH_SIZE"), "_ZN12_GLOBAL__N_1")
+        write, name_w = _counter_kib(csv_of(stem, "WRITE_SIZE"), "_ZN12_GLOBAL__N_1")
+        if name != name_w:
+            raise ValueError(f"{key}: FETCH_SIZE run profiled {name}, WRITE_SIZE run {name_w}")
+        hbm = 1024 * (fetch * fetch_factor + write * write_factor)
+        algorithmic = attention_bytes(batch, heads, seq_len, 64)
+        qkv = 6 * batch * heads * seq_len * 64
+        summary["kernels"][key] = {
+            "kernel": name, "fetch_kib_raw": round(fetch, 1), "write_kib_raw": round(write, 1),
+            "hbm_bytes": int(round(hbm)), "algorithmic_bytes": int(algorithmic),
+            "ratio": round(hbm / algorithmic, 3),
+            "fetch_vs_qkv": round(1024 * fetch * fetch_factor / qkv, 3),
+            "write_vs_o": round(1024 * write * write_factor / (qkv / 3), 3)}
+    with open(TRAFFIC_FILE, "w") as f:
+        json.dump(summary, f, indent=1)
+        f.write("\n")
+    print(json.dumps({"traffic_summary": TRAFFIC_FILE, "keys": sorted(summary["kernels"])}))
+    return 0
 
 
 def run_copy_calibration(args):
@@ -356,7 +436,13 @@ def main() -> int:
     parser.add_argument("--only", choices=sorted(WORKLOADS) + ["copy", "gemm"],
                         help="time one workload only (for profilers); prints its own JSON line")
     parser.add_argument("--mode", choices=("noncausal", "causal", "both"), default="both")
+    parser.add_argument("--traffic-from", metavar="DIR",
+                        help="write profiles/hbm_traffic.json from the rocprofv3 counter runs in DIR "
+                             "(no GPU work)")
     args = parser.parse_args()
+
+    if args.traffic_from:
+        return write_traffic_summary(args.traffic_from)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the attention forward shards over "

@@ -95,4 +95,44 @@ def test_more_than_one_gpu_is_refused():
 
 def test_traffic_keys_are_in_the_committed_summary():
     for key in bench.traffic_keys():
-        assert bench.measured_traffic(key) is not None, key
+        _, status = bench.measured_traffic(key)
+        assert status in ("current", "stale"), (key, status)
+
+
+def _write_counter_csv(path, rows):
+    path.parent.mkdir(parents=True, exist_ok=True)
+    header = ("Correlation_Id,Dispatch_Id,Kernel_Name,Counter_Name,Counter_Value\n")
+    body = "".join(f'{i},{i},"{name}","C",{value}\n' for i, (name, value) in enumerate(rows))
+    path.write_text(header + body)
+
+
+def test_traffic_summary_is_calibrated_and_stamped(tmp_path, monkeypatch):
+    # Synthetic rocprofv3 counter CSVs: the copy reads half its bytes in FETCH_SIZE (factor
+    # 2) and all of them in WRITE_SIZE; every attention key fetches 1.5x Q+K+V and writes O.
+    summary_file = tmp_path / "hbm_traffic.json"
+    monkeypatch.setattr(bench, "TRAFFIC_FILE", str(summary_file))
+    copy_kib = bench.COPY_CALIBRATION_BYTES / 1024
+    _write_counter_csv(tmp_path / "copy_both_FETCH_SIZE" / "run_counter_collection.csv",
+                       [(bench.COPY_KERNEL, copy_kib / 2)] * 3)
+    _write_counter_csv(tmp_path / "copy_both_WRITE_SIZE" / "run_counter_collection.csv",
+                       [(bench.COPY_KERNEL, copy_kib)] * 3)
+    expected = {}
+    for key in bench.traffic_keys():
+        workload, mode = key.split("/")
+        b, h, n, _ = bench.WORKLOADS[workload]
+        qkv_kib = 6 * b * h * n * 64 / 1024
+        kernel = f"_ZN12_GLOBAL__N_1kernel_{mode}"
+        # a torch helper kernel in the same run is ignored; the median dispatch is taken
+        _write_counter_csv(tmp_path / f"{workload}_{mode}_FETCH_SIZE" / "run_counter_collection.csv",
+                           [("torch_fill", 1e9), (kernel, 0.75 * qkv_kib), (kernel, 0.75 * qkv_kib), (kernel, 9e9)])
+        _write_counter_csv(tmp_path / f"{workload}_{mode}_WRITE_SIZE" / "run_counter_collection.csv",
+                           [(kernel, qkv_kib / 3)] * 2)
+        expected[key] = int(round(1024 * (1.5 * qkv_kib + qkv_kib / 3)))
+    assert bench.write_traffic_summary(str(tmp_path)) == 0
+    for key, hbm in expected.items():
+        assert bench.measured_traffic(key) == (hbm, "current")
+    # A summary taken on another version of the kernel source is reported as stale.
+    monkeypatch.setattr(bench, "kernel_source_digest", lambda: "0" * 64)
+    for key in expected:
+        assert bench.measured_traffic(key) == (None, "stale")
+    assert bench.roofline(1e12, 1.0, bench.traffic_keys()[0])["traffic"] is None

@@ -601,7 +601,8 @@ void fa2_forward_d64_kernel(const _Float16* __restrict__ query,
     // its row. The wave's 32 rows go through its 4 KiB of stage 3 (free after the last
     // tile's barrier; chunk c of row r at c ^ (r & 7)) and are stored as whole rows.
     const float inv_l = 1.0f / sum_across_halves(l_run);
-    uint8_t* const out_lds = stage3 + wave * 4096;
+    static_assert(kWaves * kQueriesPerWave * kRowBytes <= kStageBytes, "every wave's output block fits stage 3");
+    uint8_t* const out_lds = stage3 + wave * (kQueriesPerWave * kRowBytes);
 #pragma unroll
     for (int dblk = 0; dblk < 2; ++dblk)
 #pragma unroll

@@ -36,15 +36,32 @@ from oracle import attention_reference_fp32
 
 pytestmark = pytest.mark.gpu
 
-ENTRY = fa.flash_attention_cuda.tensorcore_attention_forward_production_128x128
+PRODUCTION = fa.flash_attention_cuda.tensorcore_attention_forward_production_128x128
+KEY_TILE_16 = fa.flash_attention_cuda.tensorcore_attention_forward  # noncausal, N % 16 == 0
 
+
+def ENTRY(q, k, v, causal):
+    """The production entry; sequence lengths that are not a multiple of 128 go through the
+    key-tile-16 entry (noncausal only), whose partial last query block and key tile run the
+    kernels' partial-tile builds."""
+    if q.shape[2] % 128 == 0:
+        return PRODUCTION(q, k, v, causal)
+    assert not causal
+    return KEY_TILE_16(q, k, v)
+
+
+# Every kernel the forward entries route to, and the partial-tile builds of the two key-split
+# kernels that sequence lengths off the 32-key grid reach.
 SHAPES = [
     ((1, 8, 1024), False, capi.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES), ((1, 8, 1024), True, capi.FA2_KERNEL_KEY_SPLIT_PAIRS16),
     ((1, 8, 768), False, capi.FA2_KERNEL_KEY_SPLIT_64),
+    ((1, 9, 1024), False, capi.FA2_KERNEL_KEY_SPLIT_32), ((1, 8, 384), True, capi.FA2_KERNEL_KEY_SPLIT_32),
     ((1, 64, 1024), False, capi.FA2_KERNEL_128_QUERY), ((1, 64, 1024), True, capi.FA2_KERNEL_128_QUERY),
     ((8, 16, 1024), False, capi.FA2_KERNEL_256_QUERY), ((8, 64, 1024), True, capi.FA2_KERNEL_256_QUERY),
     ((8, 64, 512), True, capi.FA2_KERNEL_256_QUERY_PAIRS), ((1, 4, 2048), False, capi.FA2_KERNEL_KEY_SPLIT_8_WAVES),
+    ((1, 2, 4096), True, capi.FA2_KERNEL_KEY_SPLIT_8_WAVES),
     ((1, 5, 8192), True, capi.FA2_KERNEL_128_QUERY_SPLIT_PAIRS),
+    ((1, 8, 2000), False, capi.FA2_KERNEL_KEY_SPLIT_32), ((1, 3, 2000), False, capi.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES),
 ]
 IDS = [f"{'causal' if c else 'noncausal'}-{b}x{h}x{n}" for (b, h, n), c, _ in SHAPES]
 

@@ -26,6 +26,7 @@ FA2_STATUS_BAD_SEQUENCE_LENGTH = 4
 FA2_STATUS_MISALIGNED = 5
 FA2_STATUS_TOO_LARGE = 6
 FA2_STATUS_BAD_KEY_TILE = 7
+FA2_STATUS_BAD_KERNEL = 8
 FA2_STATUS_HIP_ERROR_BASE = 1000
 
 # Kernels of the FP16 forward entries (fa2_forward_plan).
@@ -89,6 +90,12 @@ def _load() -> ctypes.CDLL:
     lib.fa2_abi_version.restype = ctypes.c_int
     lib.fa2_forward_plan.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int]
     lib.fa2_forward_plan.restype = ctypes.c_int
+    lib.fa2_forward_with_kernel.argtypes = [
+        ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+        ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+        ctypes.c_int, ctypes.c_void_p,
+    ]
+    lib.fa2_forward_with_kernel.restype = ctypes.c_int
     return lib
 
 
@@ -140,6 +147,35 @@ def forward_production_128x128(query: torch.Tensor, key: torch.Tensor, value: to
     )
     if status != FA2_STATUS_SUCCESS:
         raise Fa2Error("fa2_forward_production_128x128", status, status_string(status))
+    return output
+
+
+def forward_with_kernel_raw(kernel: int, query_ptr: int, key_ptr: int, value_ptr: int,
+                            output_ptr: int, batch: int, heads: int, seq_len: int, head_dim: int,
+                            causal: bool, stream: int | None) -> int:
+    """Direct call of fa2_forward_with_kernel; returns the status code."""
+    return lib.fa2_forward_with_kernel(
+        kernel, query_ptr, key_ptr, value_ptr, output_ptr, batch, heads, seq_len, head_dim,
+        1 if causal else 0, stream,
+    )
+
+
+def forward_with_kernel(kernel: int, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                        causal: bool, *, output: torch.Tensor | None = None,
+                        stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+    """The production forward on a chosen FA2_KERNEL_* (Fa2Error with status
+    FA2_STATUS_BAD_KERNEL when that kernel does not compute these sizes)."""
+    if output is None:
+        output = torch.empty_like(query)
+    if stream is None:
+        stream = torch.cuda.current_stream(query.device)
+    batch, heads, seq_len, head_dim = query.shape
+    status = forward_with_kernel_raw(
+        kernel, query.data_ptr(), key.data_ptr(), value.data_ptr(), output.data_ptr(),
+        batch, heads, seq_len, head_dim, causal, stream.cuda_stream,
+    )
+    if status != FA2_STATUS_SUCCESS:
+        raise Fa2Error("fa2_forward_with_kernel", status, status_string(status))
     return output
 
 

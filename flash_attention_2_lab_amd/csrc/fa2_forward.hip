@@ -2505,6 +2505,30 @@ fa2_forward_kernel choose_kernel(int64_t batch_heads, int64_t seq_len, bool caus
 
 bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) != 0; }
 
+// Whether `kernel` computes these sizes (a sequence length the production entry accepts,
+// a multiple of 128): the shapes each kernel's indexing, tile counts and schedules are
+// written for, whether or not choose_kernel routes them there. The 256-query kernel
+// fetches three 64-key tiles ahead (N a multiple of 256); its pairs take two 256-query
+// tiles per workgroup (causal, N a multiple of 512); the split pairs pair 128-query tiles
+// and split each pair's keys over two wave groups (causal, N a multiple of 256, from 1024
+// keys); the paired 16-query kernel pairs 16-query blocks (causal, N a multiple of 64,
+// from 512 keys); the DMA-waves kernel is noncausal. The 128-query and key-split kernels
+// take every such length in both modes.
+bool kernel_handles(int kernel, int64_t seq_len, bool causal) {
+    switch (kernel) {
+        case FA2_KERNEL_256_QUERY: return seq_len % 256 == 0;
+        case FA2_KERNEL_256_QUERY_PAIRS: return causal && seq_len % 512 == 0;
+        case FA2_KERNEL_128_QUERY: return seq_len % 128 == 0;
+        case FA2_KERNEL_128_QUERY_SPLIT_PAIRS: return causal && seq_len % 256 == 0 && seq_len >= 1024;
+        case FA2_KERNEL_KEY_SPLIT_64:
+        case FA2_KERNEL_KEY_SPLIT_32:
+        case FA2_KERNEL_KEY_SPLIT_8_WAVES: return true;
+        case FA2_KERNEL_KEY_SPLIT_PAIRS16: return causal && seq_len % 64 == 0 && seq_len >= kPairs16MinKeys;
+        case FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES: return !causal;
+        default: return false;
+    }
+}
+
 
 // Shared argument checks and dispatch of the C entry points. `multiple` is the
 // divisor seq_len must have; sequence lengths that are multiples of 256 or 128 run
@@ -2512,7 +2536,7 @@ bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) !
 // key-split kernel (which handles partial query blocks and key tiles).
 int forward(const void* query, const void* key, const void* value, void* output, int64_t batch,
             int64_t heads, int64_t seq_len, int64_t head_dim, int64_t multiple, bool causal,
-            void* stream) {
+            void* stream, int forced_kernel = FA2_KERNEL_NONE) {
     if (batch < 0 || heads < 0 || seq_len < 0 || head_dim < 0) return FA2_STATUS_NEGATIVE_DIMENSION;
     if (head_dim != kHeadDim) return FA2_STATUS_BAD_HEAD_DIM;
     if (seq_len % multiple != 0) return FA2_STATUS_BAD_SEQUENCE_LENGTH;
@@ -2528,11 +2552,14 @@ int forward(const void* query, const void* key, const void* value, void* output,
     const int64_t query_blocks = (seq_len + kQueriesPerWave - 1) / kQueriesPerWave;
     if (batch_heads > (int64_t)UINT32_MAX / query_blocks) return FA2_STATUS_TOO_LARGE;
 
+    if (forced_kernel != FA2_KERNEL_NONE && !kernel_handles(forced_kernel, seq_len, causal))
+        return FA2_STATUS_BAD_KERNEL;
+
     const float scale = 1.0f / sqrtf((float)kHeadDim);           // reference :3040-3046
     const float scale_log2 = scale * 1.4426950408889634074f;     // fold log2(e) for exp2
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipError_t err;
-    switch (choose_kernel(batch_heads, seq_len, causal)) {
+    switch (forced_kernel != FA2_KERNEL_NONE ? (fa2_forward_kernel)forced_kernel : choose_kernel(batch_heads, seq_len, causal)) {
         case FA2_KERNEL_256_QUERY:
             err = causal ? launch_wide<true, false>(query, key, value, output, batch_heads, seq_len, scale_log2, s)
                          : launch_wide<false, false>(query, key, value, output, batch_heads, seq_len, scale_log2, s);
@@ -2588,6 +2615,15 @@ extern "C" int fa2_forward_tensorcore(const void* query, const void* key, const 
                    /*causal=*/false, stream);
 }
 
+extern "C" int fa2_forward_with_kernel(int kernel, const void* query, const void* key,
+                                       const void* value, void* output, int64_t batch,
+                                       int64_t heads, int64_t seq_len, int64_t head_dim,
+                                       int causal, void* stream) {
+    if (kernel <= FA2_KERNEL_NONE || kernel > FA2_KERNEL_128_QUERY_SPLIT_PAIRS) return FA2_STATUS_BAD_KERNEL;
+    return forward(query, key, value, output, batch, heads, seq_len, head_dim, kQueryTileAlign,
+                   causal != 0, stream, kernel);
+}
+
 extern "C" const char* fa2_status_string(int status) {
     switch (status) {
         case FA2_STATUS_SUCCESS: return "success";
@@ -2598,6 +2634,7 @@ extern "C" const char* fa2_status_string(int status) {
         case FA2_STATUS_MISALIGNED: return "tensor pointer not 16-byte aligned";
         case FA2_STATUS_TOO_LARGE: return "problem too large for the kernel's launch grid";
         case FA2_STATUS_BAD_KEY_TILE: return "key tile must be 16 or 32";
+        case FA2_STATUS_BAD_KERNEL: return "kernel does not compute these sizes";
         default: break;
     }
     if (status > FA2_STATUS_HIP_ERROR_BASE)

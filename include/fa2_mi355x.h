@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define FA2_MI355X_ABI_VERSION 7
+#define FA2_MI355X_ABI_VERSION 8
 
 enum fa2_status {
     FA2_STATUS_SUCCESS = 0,
@@ -39,6 +39,8 @@ enum fa2_status {
     FA2_STATUS_MISALIGNED = 5,          /* a pointer below the entry's alignment             */
     FA2_STATUS_TOO_LARGE = 6,           /* seq_len > 2^24 or launch grid beyond 2^32 groups */
     FA2_STATUS_BAD_KEY_TILE = 7,        /* fa2_forward_tensorcore: key_tile not 16 or 32     */
+    FA2_STATUS_BAD_KERNEL = 8,          /* fa2_forward_with_kernel: the kernel does not      */
+                                        /* compute these sizes                               */
     FA2_STATUS_HIP_ERROR_BASE = 1000    /* + hipError_t from the launch                      */
 };
 
@@ -158,6 +160,26 @@ enum fa2_forward_kernel {
  * for callers and tests that need to know which schedule a shape gets.
  */
 int fa2_forward_plan(int64_t batch, int64_t heads, int64_t seq_len, int causal);
+
+/*
+ * fa2_forward_production_128x128 run on a chosen kernel instead of the one
+ * fa2_forward_plan names: the same checks, arithmetic and output contract, then
+ * FA2_STATUS_BAD_KERNEL unless `kernel` computes these sizes:
+ *   FA2_KERNEL_256_QUERY               seq_len % 256 == 0
+ *   FA2_KERNEL_256_QUERY_PAIRS         causal, seq_len % 512 == 0
+ *   FA2_KERNEL_128_QUERY               any (seq_len % 128 == 0)
+ *   FA2_KERNEL_128_QUERY_SPLIT_PAIRS   causal, seq_len % 256 == 0, seq_len >= 1024
+ *   FA2_KERNEL_KEY_SPLIT_64, _32, _8_WAVES   any
+ *   FA2_KERNEL_KEY_SPLIT_PAIRS16       causal, seq_len % 64 == 0, seq_len >= 512
+ *   FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES  noncausal
+ * No counterpart in the reference (whose production entry has one kernel): it is for
+ * re-measuring the kernel choice - timing the kernels on either side of each routing
+ * threshold - and for tests that hold every kernel to the oracle on shapes it is not
+ * routed to.
+ */
+int fa2_forward_with_kernel(int kernel, const void* query, const void* key, const void* value,
+                            void* output, int64_t batch, int64_t heads, int64_t seq_len,
+                            int64_t head_dim, int causal, void* stream);
 
 #ifdef __cplusplus
 }

@@ -98,11 +98,43 @@ int main(void) {
     CHECK(tensorcore(fake[0] + 8, 1, 1, 48, 64, 16) == FA2_STATUS_MISALIGNED, "tensorcore misaligned query");
     CHECK(tensorcore(NULL, 0, 1, 48, 64, 16) == FA2_STATUS_SUCCESS, "tensorcore empty batch");
 
+    /* fa2_forward_with_kernel: an unknown kernel id is rejected first; a known one goes through
+     * the production checks (a null query stops it before any launch), then its domain. Only
+     * sizes outside the chosen kernel's domain get past the pointer checks here. */
+    for (int kernel = -2; kernel <= 12; ++kernel)
+        for (int causal = 0; causal <= 1; ++causal) {
+            const int known = kernel >= FA2_KERNEL_256_QUERY && kernel <= FA2_KERNEL_128_QUERY_SPLIT_PAIRS;
+            const int status = fa2_forward_with_kernel(kernel, NULL, k, v, o, 1, 1, 1024, 64, causal, NULL);
+            CHECK(status == (known ? FA2_STATUS_NULL_POINTER : FA2_STATUS_BAD_KERNEL), "kernel %d: status %d",
+                  kernel, status);
+        }
+    const int64_t lengths[] = {128, 256, 384, 512, 640, 768, 896, 1024, 1152, 1280, 2048, 4096};
+    for (size_t i = 0; i < sizeof(lengths) / sizeof(lengths[0]); ++i)
+        for (int causal = 0; causal <= 1; ++causal) {
+            const int64_t n = lengths[i];
+            const int outside[] = {
+                n % 256 != 0 ? FA2_KERNEL_256_QUERY : 0,
+                !causal || n % 512 != 0 ? FA2_KERNEL_256_QUERY_PAIRS : 0,
+                !causal || n % 256 != 0 || n < 1024 ? FA2_KERNEL_128_QUERY_SPLIT_PAIRS : 0,
+                !causal || n % 64 != 0 || n < 512 ? FA2_KERNEL_KEY_SPLIT_PAIRS16 : 0,
+                causal ? FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES : 0};
+            for (size_t j = 0; j < sizeof(outside) / sizeof(outside[0]); ++j)
+                if (outside[j])
+                    CHECK(fa2_forward_with_kernel(outside[j], q, k, v, o, 1, 1, n, 64, causal, NULL) ==
+                              FA2_STATUS_BAD_KERNEL,
+                          "kernel %d outside its domain at %lld keys causal=%d", outside[j], (long long)n, causal);
+        }
+    CHECK(fa2_forward_with_kernel(FA2_KERNEL_256_QUERY, q, k, v, o, 1, 1, 100, 64, 0, NULL) ==
+              FA2_STATUS_BAD_SEQUENCE_LENGTH, "forced kernel, seq_len 100");
+    CHECK(fa2_forward_with_kernel(FA2_KERNEL_256_QUERY, q, k, v, o, INT64_MAX, INT64_MAX, 256, 64, 0, NULL) ==
+              FA2_STATUS_TOO_LARGE, "forced kernel, sizes beyond the grid");
+
     /* Every status has a text; unknown codes have one too (static storage, never NULL). */
     const int codes[] = {FA2_STATUS_SUCCESS, FA2_STATUS_NULL_POINTER, FA2_STATUS_NEGATIVE_DIMENSION,
                          FA2_STATUS_BAD_HEAD_DIM, FA2_STATUS_BAD_SEQUENCE_LENGTH, FA2_STATUS_MISALIGNED,
-                         FA2_STATUS_TOO_LARGE, FA2_STATUS_BAD_KEY_TILE, FA2_STATUS_HIP_ERROR_BASE + 1,
-                         FA2_STATUS_HIP_ERROR_BASE + 98, -1, 8, 999, INT32_MAX, INT32_MIN};
+                         FA2_STATUS_TOO_LARGE, FA2_STATUS_BAD_KEY_TILE, FA2_STATUS_BAD_KERNEL,
+                         FA2_STATUS_HIP_ERROR_BASE + 1, FA2_STATUS_HIP_ERROR_BASE + 98, -1, 9, 999,
+                         INT32_MAX, INT32_MIN};
     for (size_t i = 0; i < sizeof(codes) / sizeof(codes[0]); ++i) {
         const char* text = fa2_status_string(codes[i]);
         CHECK(text != NULL && strlen(text) > 0, "status %d has no text", codes[i]);

@@ -31,7 +31,7 @@ def test_status_codes_match_header():
     text = capi.HEADER_PATH.read_text()
     for name in ("SUCCESS", "NULL_POINTER", "NEGATIVE_DIMENSION", "BAD_HEAD_DIM",
                  "BAD_SEQUENCE_LENGTH", "MISALIGNED", "TOO_LARGE", "BAD_KEY_TILE",
-                 "HIP_ERROR_BASE"):
+                 "BAD_KERNEL", "HIP_ERROR_BASE"):
         value = int(re.search(rf"FA2_STATUS_{name} = (\d+)", text).group(1))
         assert getattr(capi, f"FA2_STATUS_{name}") == value
 
@@ -110,6 +110,7 @@ def test_forward_plan_follows_the_measured_thresholds(batch, heads, seq_len, cau
     (capi.FA2_STATUS_BAD_HEAD_DIM, "head dimension must equal 64"),
     (capi.FA2_STATUS_BAD_SEQUENCE_LENGTH, "sequence length not a multiple of the entry's key tile"),
     (capi.FA2_STATUS_BAD_KEY_TILE, "key tile must be 16 or 32"),
+    (capi.FA2_STATUS_BAD_KERNEL, "kernel does not compute these sizes"),
     (capi.FA2_STATUS_NULL_POINTER, "null tensor pointer"),
     (capi.FA2_STATUS_MISALIGNED, "tensor pointer not 16-byte aligned"),
     (999, "unknown status"),
@@ -193,3 +194,37 @@ def test_tensorcore_entry_shares_the_other_checks():
     assert _call_tc(seq_len=0) == capi.FA2_STATUS_SUCCESS
     assert _call_tc(ptrs=(4096, 4104, 4096, 4096)) == capi.FA2_STATUS_MISALIGNED
     assert _call_tc(seq_len=1 << 30, ptrs=(4096,) * 4) == capi.FA2_STATUS_TOO_LARGE
+
+
+def _call_with(kernel, batch=1, heads=1, seq_len=128, head_dim=64, causal=False, ptrs=(4096,) * 4):
+    # Aligned, non-null pointers that are never dereferenced: every call here is rejected
+    # before a launch.
+    q, k, v, o = ptrs
+    return capi.forward_with_kernel_raw(kernel, q, k, v, o, batch, heads, seq_len, head_dim, causal, None)
+
+
+@pytest.mark.parametrize("kernel, seq_len, causal", [
+    (capi.FA2_KERNEL_256_QUERY, 128, False), (capi.FA2_KERNEL_256_QUERY, 384, True),
+    (capi.FA2_KERNEL_256_QUERY_PAIRS, 1024, False), (capi.FA2_KERNEL_256_QUERY_PAIRS, 768, True),
+    (capi.FA2_KERNEL_128_QUERY_SPLIT_PAIRS, 8192, False), (capi.FA2_KERNEL_128_QUERY_SPLIT_PAIRS, 768, True),
+    (capi.FA2_KERNEL_128_QUERY_SPLIT_PAIRS, 1152, True),
+    (capi.FA2_KERNEL_KEY_SPLIT_PAIRS16, 1024, False), (capi.FA2_KERNEL_KEY_SPLIT_PAIRS16, 384, True),
+    (capi.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES, 1024, True),
+    (capi.FA2_KERNEL_NONE, 1024, False), (10, 1024, False), (-1, 1024, True), (1000, 1024, False),
+])
+def test_forced_kernel_rejects_sizes_it_does_not_compute(kernel, seq_len, causal):
+    assert _call_with(kernel, seq_len=seq_len, causal=causal) == capi.FA2_STATUS_BAD_KERNEL
+
+
+def test_forced_kernel_shares_the_production_checks_first():
+    # The entry's own checks come before the kernel's domain, in the production order.
+    k = capi.FA2_KERNEL_256_QUERY
+    assert _call_with(k, head_dim=32) == capi.FA2_STATUS_BAD_HEAD_DIM
+    assert _call_with(k, batch=-1) == capi.FA2_STATUS_NEGATIVE_DIMENSION
+    assert _call_with(k, seq_len=100) == capi.FA2_STATUS_BAD_SEQUENCE_LENGTH
+    assert _call_with(k, seq_len=0) == capi.FA2_STATUS_SUCCESS
+    assert _call_with(k, ptrs=(0, 4096, 4096, 4096)) == capi.FA2_STATUS_NULL_POINTER
+    assert _call_with(k, ptrs=(4096, 4104, 4096, 4096)) == capi.FA2_STATUS_MISALIGNED
+    assert _call_with(k, seq_len=1 << 31) == capi.FA2_STATUS_TOO_LARGE
+    # An unknown kernel id is rejected before anything else.
+    assert _call_with(0, head_dim=32) == capi.FA2_STATUS_BAD_KERNEL

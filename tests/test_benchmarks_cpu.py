@@ -118,6 +118,13 @@ def test_bench_traffic_keys_are_measured():
     keys = set(bench.traffic_keys())
     assert {"b1h8n1024/noncausal", "b1h8n1024/causal", "b16h16n4096/noncausal", "b16h16n4096/causal",
             "b2h32n16384/causal"} <= keys
+    import json
+
+    summary = json.loads(Path(bench.TRAFFIC_FILE).read_text())
+    assert len(summary["source_sha256"]) == 64  # the kernel source it was measured on
     for key in sorted(keys):
-        traffic = bench.measured_traffic(key)
-        assert isinstance(traffic, int) and traffic > 0, key
+        entry = summary["kernels"][key]
+        assert isinstance(entry["hbm_bytes"], int) and entry["hbm_bytes"] > 0, key
+        # Reported only while the kernel source is the profiled one (else null, "stale").
+        traffic, status = bench.measured_traffic(key)
+        assert (traffic, status) in ((entry["hbm_bytes"], "current"), (None, "stale")), key

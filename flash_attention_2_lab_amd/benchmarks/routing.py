@@ -55,14 +55,22 @@ CASES = (
     Case("wide vs 128-query, noncausal: whole rounds", 16, 16, 4096, False, (K.FA2_KERNEL_256_QUERY, K.FA2_KERNEL_128_QUERY)),
     Case("wide vs 128-query, causal: 256 workgroups", 1, 32, 4096, True, (K.FA2_KERNEL_256_QUERY, K.FA2_KERNEL_128_QUERY)),
     Case("wide vs 128-query, causal: 512 workgroups", 1, 64, 4096, True, (K.FA2_KERNEL_256_QUERY, K.FA2_KERNEL_128_QUERY)),
-    Case("head groups vs pairs, causal: T = 4, 1024 tiles", 16, 16, 1024, True, (K.FA2_KERNEL_256_QUERY, K.FA2_KERNEL_256_QUERY_PAIRS)),
-    Case("head groups vs pairs, causal: T = 8", 8, 16, 2048, True, (K.FA2_KERNEL_256_QUERY, K.FA2_KERNEL_256_QUERY_PAIRS)),
-    Case("head groups vs pairs, causal: throughput shape", 16, 16, 4096, True, (K.FA2_KERNEL_256_QUERY, K.FA2_KERNEL_256_QUERY_PAIRS)),
-    Case("split pairs vs 128-query, causal: 4096 keys", 1, 16, 4096, True, (K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS, K.FA2_KERNEL_128_QUERY)),
+    Case("pairs vs head groups, causal: T = 4, 1024 tiles", 16, 16, 1024, True, (K.FA2_KERNEL_256_QUERY, K.FA2_KERNEL_256_QUERY_PAIRS)),
+    Case("pairs vs head groups, causal: T = 4, 2048 tiles", 32, 16, 1024, True, (K.FA2_KERNEL_256_QUERY, K.FA2_KERNEL_256_QUERY_PAIRS)),
+    Case("pairs vs head groups, causal: T = 8", 8, 16, 2048, True, (K.FA2_KERNEL_256_QUERY, K.FA2_KERNEL_256_QUERY_PAIRS)),
+    Case("head groups vs pairs, causal: T = 16 (throughput shape)", 16, 16, 4096, True, (K.FA2_KERNEL_256_QUERY, K.FA2_KERNEL_256_QUERY_PAIRS)),
+    Case("head groups vs pairs, causal: T = 64", 2, 32, 16384, True, (K.FA2_KERNEL_256_QUERY, K.FA2_KERNEL_256_QUERY_PAIRS)),
+    Case("pairs vs head groups, causal: T = 2, 2048 tiles", 64, 16, 512, True, (K.FA2_KERNEL_256_QUERY, K.FA2_KERNEL_256_QUERY_PAIRS)),
+    Case("head groups vs pairs, causal: T = 2, 4096 tiles", 128, 16, 512, True, (K.FA2_KERNEL_256_QUERY, K.FA2_KERNEL_256_QUERY_PAIRS)),
+    Case("128-query vs split pairs, causal: 2048 keys", 1, 32, 2048, True, (K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS, K.FA2_KERNEL_128_QUERY)),
+    Case("split pairs vs 128-query, causal: 4096 keys, 320 groups", 1, 10, 4096, True, (K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS, K.FA2_KERNEL_128_QUERY)),
+    Case("split pairs vs 128-query, causal: 4096 keys, 512 groups", 1, 16, 4096, True, (K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS, K.FA2_KERNEL_128_QUERY)),
+    Case("key-split vs split pairs, causal: 4096 keys, 256 groups", 1, 8, 4096, True, (K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS, K.FA2_KERNEL_KEY_SPLIT_32)),
     Case("split pairs vs 128-query, causal: 8192 keys", 1, 8, 8192, True, (K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS, K.FA2_KERNEL_128_QUERY)),
     Case("split pairs vs 128-query, causal: 16384 keys", 1, 4, 16384, True, (K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS, K.FA2_KERNEL_128_QUERY)),
-    Case("128-query vs key-split, noncausal: 256 groups", 1, 32, 1024, False, (K.FA2_KERNEL_128_QUERY, K.FA2_KERNEL_KEY_SPLIT_32)),
-    Case("128-query vs key-split, noncausal: 248 groups", 1, 31, 1024, False, (K.FA2_KERNEL_128_QUERY, K.FA2_KERNEL_KEY_SPLIT_32)),
+    Case("128-query vs key-split, noncausal: 200 groups", 1, 25, 1024, False, (K.FA2_KERNEL_128_QUERY, K.FA2_KERNEL_KEY_SPLIT_32)),
+    Case("key-split vs 128-query, noncausal: 192 groups", 1, 24, 1024, False, (K.FA2_KERNEL_128_QUERY, K.FA2_KERNEL_KEY_SPLIT_32)),
+    Case("key-split vs 128-query, noncausal: 192 groups of 4096 keys", 1, 6, 4096, False, (K.FA2_KERNEL_128_QUERY, K.FA2_KERNEL_KEY_SPLIT_32)),
     Case("128-query vs key-split, causal: 320 groups", 1, 40, 1024, True, (K.FA2_KERNEL_128_QUERY, K.FA2_KERNEL_KEY_SPLIT_32)),
     Case("128-query vs key-split, causal: 256 groups", 1, 32, 1024, True, (K.FA2_KERNEL_128_QUERY, K.FA2_KERNEL_KEY_SPLIT_32)),
     Case("paired 16-query vs key-split, causal: 512 keys", 1, 8, 512, True, (K.FA2_KERNEL_KEY_SPLIT_PAIRS16, K.FA2_KERNEL_KEY_SPLIT_32)),

@@ -2371,20 +2371,28 @@ hipError_t launch_split_pairs(const void* q, const void* k, const void* v, void*
                                                              q, k, v, o, (int)seq_len, (int)query_tiles, scale_log2);
 }
 
-// Causal 256-query problems run one query tile per workgroup in the level order of
-// xcd_work_item when the grid has enough tiles to balance and the XCDs get about
-// equal work; otherwise pairs of tiles (T even), which give every workgroup the same
-// work. Measured on MI355X (same process, pairs -> head groups): -4% to -5% at 1024
-// tiles with T >= 8 (B8 H16 N2048, B4 H16 N4096, B1 H64 N4096), -2% to -4% at 2048
-// tiles (B32 H16 N1024, B16 H16 N2048, B8 H16 N4096), -1% to -3% at 4096 (B16 H16
-// N4096, B2 H32 N16384); +2% at B16 H16 N1024 (1024 tiles of T = 4). When batch*heads
-// is not a multiple of 8 the XCD ranges split heads, and an XCD whose range holds a
-// split head's heavy tiles gets more work: up to 8/batch_heads of a head's share more
-// (5.5% at 36 heads; 82% for one head), so single tiles need 32 heads or more there:
-// -28% to -32% at B1 H66 N4096 and B1 H130 N2048 (with the level order).
+// Causal 256-query problems with T = 4 or 8 query tiles per head, or T = 2 below 4096
+// tiles, run pairs of tiles (T-1-p, then p) per workgroup, which give every workgroup
+// the same work; otherwise (T odd, T >= 16, or T = 2 from 4096 tiles) one query tile
+// per workgroup in the level order of xcd_work_item (per-XCD head groups), whose
+// workgroups share each head's K/V through one L2 (HBM fetch 1.05x Q+K+V at B16 H16
+// N4096 against 1.8x for pairs). Re-measured on MI355X with the K and V^T reads issued
+// ahead of their phases (same process, graph replays, head groups -> pairs): -7% to -8%
+// at T = 4 (B32 H16 N1024, B8 H64 N1024), -6% at T = 8 with 1024 tiles (B8 H16 N2048),
+// -1.4% to -3% at T = 8 (B16 H16 N2048, B4 H64 N2048, B16 H32 N2048, B32 H16 N2048);
+// at T = 16 to 64 within 0 to -2% (B16 H16 N4096: 0; B4 H16 N4096, B1 H64 N4096, B2 H16
+// N8192, B2 H32 N16384), where the groups' lower traffic is kept; at T = 2, -3.7% at
+// 2048 tiles (B64 H16 N512) but +2.6% at 4096 (B128 H16 N512). Before that schedule
+// change the head groups measured 1-6% faster than pairs from T = 8 or 2048 tiles on.
+// When batch*heads is not a multiple of 8 the XCD ranges split heads, and an XCD whose
+// range holds a split head's heavy tiles gets more work: up to 8/batch_heads of a head's
+// share more (5.5% at 36 heads; 82% for one head), so single tiles need 32 heads or more
+// there: -28% to -32% at B1 H66 N4096 and B1 H130 N2048 (with the level order).
 bool use_head_groups(int64_t batch_heads, int64_t tiles_per_head) {
+    if (tiles_per_head % 2 != 0) return true;
     if (batch_heads % 8 != 0 && batch_heads < 32) return false;
-    return tiles_per_head >= 8 || batch_heads * tiles_per_head >= 2048;
+    if (tiles_per_head >= 16) return true;
+    return tiles_per_head == 2 && batch_heads * tiles_per_head >= 4096;
 }
 
 // 256-query workgroups (64 queries per wave) once the grid fills every workgroup
@@ -2428,8 +2436,12 @@ bool use_wide_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
 // 128-query workgroups (4 waves) when they fill the chip (two per CU); otherwise
 // the key-split kernel (one 32-query block per workgroup, keys split over 4 waves).
 // Kernel choice from measured crossovers on MI355X (B*H*N/128 = number of
-// 128-query groups): noncausal from one group per CU, causal from 320 groups (fewer
-// leave CUs idle behind the longest causal groups). Measured against the key-split
+// 128-query groups): noncausal from 200 groups, causal from 320 groups (fewer
+// leave CUs idle behind the longest causal groups). Noncausal, re-measured with the
+// routing check (same process, graph replays, key-split 32 -> 128-query): -16% to -28%
+// at 200-248 groups (B1 H25-H31 N1024, B2 H13 N1024, B1 H13-H14 N2048, B1 H7 N4096,
+// B1 H50-H60 N512), -3% to -7% at 160-192 groups of 1024 keys, +0.5% and +2.3% at 192
+// groups of 2048 and 4096 keys. Measured against the key-split
 // kernel with the causal tiles in level-ordered chunks (same process): -2% to -23% at
 // 320-504 groups (B1 H40 N1024, B1 H24 N2048, B1 H48 N1024, B1 H56 N1024, B1 H63
 // N1024; B1 H20 N2048, B1 H10 N4096, B1 H12 N4096, B1 H44 N1024, B1 H52 N1024, B1 H28
@@ -2439,7 +2451,7 @@ bool use_wide_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
 // 32-key tiles (half the LDS, two workgroups per CU) beyond.
 bool use_128_query_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
     const int64_t groups = batch_heads * (seq_len / 128);
-    return groups >= (causal ? 320 : 256);
+    return groups >= (causal ? 320 : 200);
 }
 
 // Causal problems of 320 to 512 groups of 128 queries (one round of the 128-query
@@ -2447,13 +2459,16 @@ bool use_128_query_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
 // one workgroup per CU, 160 to 256 of them). Measured on MI355X against the
 // 128-query kernel (same process, graph replays): -6% to -10% at 8192 keys (B1 H5-H8),
 // -13% to -16% at 16384 (B1 H3-H4, also with sigma = 2 logits), -16% at B1 H2 N32768;
-// -4.5% to +1% at 4096 keys (B1 H10-H16, B2 H8) and 1-14% slower at 256-2048 keys,
+// with its LDS-staged output and early K/V reads, -3% to -10% at 4096 keys (B1 H10-H16,
+// B2 H8, B3 H5), -1.5% to +3% at 2048 keys and 6-13% slower at 1024 keys,
 // where its steps and fixed costs (Q, the first tiles, the light tile's store, the
-// merge) outweigh the balance. Each wave running the 128-query kernel's software
+// merge) outweigh the balance. Below 320 groups the key-split kernel with 32-key tiles
+// was 10-35% faster at 4096-8192 keys (B1 H6-H8 N4096, B1 H3-H4 N8192) and the split
+// pairs gained at most 9% at 256 groups of 16384-32768 keys. Each wave running the 128-query kernel's software
 // pipeline instead measured 4-30% slower at every length. Beyond 512 groups the
 // 128-query kernel's level order balances its rounds, and the split pairs (several
 // rounds of one workgroup per CU) ran 20-45% slower (B1 H10-H16 N8192, B1 H5-H8 N16384).
-constexpr int64_t kSplitPairsMinKeys = 8192;
+constexpr int64_t kSplitPairsMinKeys = 4096;
 bool use_split_pairs_kernel(int64_t batch_heads, int64_t seq_len, bool causal) {
     if (!causal || seq_len % 256 != 0 || seq_len < kSplitPairsMinKeys) return false;
     const int64_t groups = batch_heads * (seq_len / 128);

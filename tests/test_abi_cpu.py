@@ -48,12 +48,12 @@ K = capi
 
 
 @pytest.mark.parametrize("batch, heads, seq_len, causal, kernel", [
-    # Noncausal: 256-query from 512 groups of 256 queries, 128-query from 256 groups of
+    # Noncausal: 256-query from 512 groups of 256 queries, 128-query from 200 groups of
     # 128, key-split below (64-key tiles up to 256 blocks of 32 queries; from 1024 keys
     # with separate DMA waves).
     (1, 128, 1024, False, K.FA2_KERNEL_256_QUERY), (1, 127, 1024, False, K.FA2_KERNEL_128_QUERY),
-    (16, 16, 4096, False, K.FA2_KERNEL_256_QUERY), (1, 32, 1024, False, K.FA2_KERNEL_128_QUERY),
-    (1, 31, 1024, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 8, 1024, False, K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES),
+    (16, 16, 4096, False, K.FA2_KERNEL_256_QUERY), (1, 25, 1024, False, K.FA2_KERNEL_128_QUERY),
+    (1, 24, 1024, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 8, 1024, False, K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES),
     (1, 9, 1024, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 8, 128, False, K.FA2_KERNEL_KEY_SPLIT_32),
     # ... except where the 256-query grid ends in a last round at most half full and
     # the 128-query kernel's finer rounds are modeled more than 5% faster.
@@ -62,26 +62,26 @@ K = capi
     (7, 16, 2048, False, K.FA2_KERNEL_256_QUERY), (6, 16, 4096, False, K.FA2_KERNEL_256_QUERY),
     # Causal: 256-query from 512 workgroups of tile pairs when a head has an even
     # number T of tiles, single tiles from 2048 with an odd number. Single tiles in
-    # level order from T >= 8 or 2048 tiles; pairs below that.
+    # level order at T >= 16 (and T = 2 from 4096 tiles); pairs at T = 4 and 8.
     (16, 16, 4096, True, K.FA2_KERNEL_256_QUERY), (1, 256, 1024, True, K.FA2_KERNEL_256_QUERY_PAIRS),
     (1, 255, 1024, True, K.FA2_KERNEL_128_QUERY), (2, 32, 16384, True, K.FA2_KERNEL_256_QUERY),
-    (32, 16, 1024, True, K.FA2_KERNEL_256_QUERY), (1, 504, 1024, True, K.FA2_KERNEL_256_QUERY_PAIRS),
-    (8, 16, 2048, True, K.FA2_KERNEL_256_QUERY), (1, 64, 4096, True, K.FA2_KERNEL_256_QUERY),
+    (32, 16, 1024, True, K.FA2_KERNEL_256_QUERY_PAIRS), (1, 504, 1024, True, K.FA2_KERNEL_256_QUERY_PAIRS),
+    (8, 16, 2048, True, K.FA2_KERNEL_256_QUERY_PAIRS), (1, 64, 4096, True, K.FA2_KERNEL_256_QUERY),
     (1, 66, 4096, True, K.FA2_KERNEL_256_QUERY), (1, 510, 1024, True, K.FA2_KERNEL_256_QUERY_PAIRS),
     (1, 410, 1280, True, K.FA2_KERNEL_256_QUERY), (1, 409, 1280, True, K.FA2_KERNEL_128_QUERY),
     (1, 64, 1024, True, K.FA2_KERNEL_128_QUERY),
-    # Causal, 320 to 512 groups of 128 with 8192 keys or more (a multiple of 256): pairs
+    # Causal, 320 to 512 groups of 128 with 4096 keys or more (a multiple of 256): pairs
     # of 128-query tiles split over two wave groups.
     (1, 8, 8192, True, K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS), (1, 5, 8192, True, K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS),
     (1, 3, 16384, True, K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS), (2, 4, 8192, True, K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS),
     (1, 2, 32768, True, K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS), (1, 9, 8192, True, K.FA2_KERNEL_128_QUERY),
-    (1, 16, 4096, True, K.FA2_KERNEL_128_QUERY), (1, 5, 8320, True, K.FA2_KERNEL_128_QUERY),
+    (1, 16, 4096, True, K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS), (1, 5, 8320, True, K.FA2_KERNEL_128_QUERY),
     (1, 4, 8192, True, K.FA2_KERNEL_KEY_SPLIT_32), (1, 8, 8192, False, K.FA2_KERNEL_128_QUERY),
     # 128-query from 320 groups of 128.
     (1, 40, 1024, True, K.FA2_KERNEL_128_QUERY), (1, 72, 512, True, K.FA2_KERNEL_KEY_SPLIT_32),
     (1, 57, 1024, True, K.FA2_KERNEL_128_QUERY), (1, 39, 1024, True, K.FA2_KERNEL_KEY_SPLIT_32),
-    (1, 12, 4096, True, K.FA2_KERNEL_128_QUERY), (1, 24, 2048, True, K.FA2_KERNEL_128_QUERY),
-    (1, 10, 4096, True, K.FA2_KERNEL_128_QUERY), (1, 8, 4096, True, K.FA2_KERNEL_KEY_SPLIT_32),
+    (1, 12, 4096, True, K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS), (1, 24, 2048, True, K.FA2_KERNEL_128_QUERY),
+    (1, 10, 4096, True, K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS), (1, 8, 4096, True, K.FA2_KERNEL_KEY_SPLIT_32),
     (1, 8, 1024, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16), (1, 2, 128, True, K.FA2_KERNEL_KEY_SPLIT_32),
     (1, 8, 896, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16), (1, 2, 1024, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16),
     (1, 8, 512, True, K.FA2_KERNEL_KEY_SPLIT_PAIRS16), (1, 8, 384, True, K.FA2_KERNEL_KEY_SPLIT_32),
@@ -97,6 +97,12 @@ K = capi
     # Sequence lengths the production entry rejects but the Bc16/Bc32 entries take
     # (partial last block) run the key-split kernel.
     (4, 64, 1040, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 2, 80, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 2, 240, False, K.FA2_KERNEL_KEY_SPLIT_64),
+    # Causal 256-query: pairs of tiles at T = 4 and 8 (T = 2 below 4096 tiles), head groups
+    # at T >= 16 or odd; split pairs from 4096 keys at 320-512 groups of 128.
+    (32, 16, 1024, True, K.FA2_KERNEL_256_QUERY_PAIRS), (8, 16, 2048, True, K.FA2_KERNEL_256_QUERY_PAIRS),
+    (16, 16, 4096, True, K.FA2_KERNEL_256_QUERY), (128, 16, 512, True, K.FA2_KERNEL_256_QUERY),
+    (64, 16, 512, True, K.FA2_KERNEL_256_QUERY_PAIRS), (1, 20, 16384, True, K.FA2_KERNEL_256_QUERY_PAIRS),
+    (1, 16, 4096, True, K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS), (1, 32, 2048, True, K.FA2_KERNEL_128_QUERY),
     # Nothing to launch.
     (0, 8, 1024, False, K.FA2_KERNEL_NONE), (1, 0, 1024, True, K.FA2_KERNEL_NONE),
     (1, 8, 0, False, K.FA2_KERNEL_NONE), (1, 1, (1 << 24) + 128, False, K.FA2_KERNEL_NONE),

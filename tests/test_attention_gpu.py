@@ -344,22 +344,26 @@ def test_scores_stepping_across_the_rescale_bound(causal, shape, step):
     (True, (8, 64, 1024), capi.FA2_KERNEL_256_QUERY), (True, (2, 64, 2048), capi.FA2_KERNEL_256_QUERY),
     (True, (4, 128, 1280), capi.FA2_KERNEL_256_QUERY), (True, (1, 410, 1280), capi.FA2_KERNEL_256_QUERY),
     (True, (8, 64, 512), capi.FA2_KERNEL_256_QUERY_PAIRS), (True, (1, 260, 1024), capi.FA2_KERNEL_256_QUERY_PAIRS),
-    (True, (1, 130, 2048), capi.FA2_KERNEL_256_QUERY), (True, (1, 66, 4096), capi.FA2_KERNEL_256_QUERY)])
+    (True, (1, 130, 2048), capi.FA2_KERNEL_256_QUERY), (True, (1, 66, 4096), capi.FA2_KERNEL_256_QUERY),
+    (True, (8, 64, 1024), capi.FA2_KERNEL_256_QUERY_PAIRS), (True, (2, 64, 2048), capi.FA2_KERNEL_256_QUERY_PAIRS)])
 def test_wide_workgroup_shapes_match_oracle(causal, shape, kernel, ramp):
     # Large enough for the 256-query kernel (64 queries per wave as two 32-query
     # blocks): every row of three whole heads - all four waves, both blocks of each
     # wave and, causal, every diagonal tile - plus sampled rows of the others. With
     # `ramp` the key norms grow 5x along the sequence, forcing the recompute path.
-    # Causal schedules: one query tile per workgroup in level order, in groups of heads
-    # per XCD (batch*heads a multiple of 8: T = 4, 8 and 5 query tiles per head here) or
-    # over XCD ranges that split heads (T = 5 with batch*heads = 410, T = 8 with 130,
-    # T = 16 with 66), and pairs of tiles T-1-p, p (T = 2; T = 4 with batch*heads = 260).
+    # Causal schedules, each run on the kernel named (fa2_forward_with_kernel; the kernel
+    # choice routes T = 4 and 8 to the pairs): one query tile per workgroup in level
+    # order, in groups of heads per XCD (batch*heads a multiple of 8: T = 4, 8 and 5 query
+    # tiles per head here) or over XCD ranges that split heads (T = 5 with batch*heads =
+    # 410, T = 8 with 130, T = 16 with 66), and pairs of tiles T-1-p, p (T = 2, 4 and 8;
+    # T = 4 with batch*heads = 260).
     batch, heads, seq_len = shape
-    assert capi.forward_plan(batch, heads, seq_len, causal) == kernel
     q, k, v = _inputs(*shape, seed=13)
     if ramp:
         k = (k.float() * torch.linspace(1.0, 5.0, seq_len).view(1, 1, -1, 1)).half()
-    out = _run(q, k, v, causal).cpu()
+    out = capi.forward_with_kernel(kernel, q.cuda(), k.cuda(), v.cuda(), causal)
+    torch.cuda.synchronize()
+    out = out.cpu()
     assert torch.isfinite(out).all()
     whole = [(0, 0), (batch - 1, heads - 1), (batch // 2, heads // 3)]
     rows = [(b, h, i) for b, h in whole for i in range(seq_len)] + _sample_rows(batch, heads, seq_len, 64, seed=14)

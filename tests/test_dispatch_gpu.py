@@ -3,13 +3,13 @@
 The forward picks its kernel from (batch*heads, seq_len, causal) (fa2_forward.hip,
 `choose_kernel`): the 256-query kernel from 512 workgroups (noncausal: unless its grid
 ends in a partial round that the 128-query kernel's finer rounds finish sooner; causal:
-one query tile per workgroup in level order (per-XCD head groups when batch*heads is a
-multiple of 8) when a head has at least 8 tiles or the grid 2048; else pairs of query
-tiles when a head has an even number of them, one tile per workgroup from 2048 when odd),
-causal problems of 320 to 512 groups of 128 queries with at least 8192 keys (a multiple of
-256) in pairs of 128-query tiles whose keys two wave groups split, the 128-query kernel
-from 256 (noncausal) or 320 (causal) groups of 128 queries, and otherwise the key-split
-kernel: up to 256 query blocks of 32, 4 waves with 64-key tiles
+pairs of query tiles at T = 4 and 8 tiles per head, at T = 2 below 4096 tiles, and at any
+even T when batch*heads is below 32 and not a multiple of 8; otherwise one query tile per
+workgroup in level order, per-XCD head groups when batch*heads is a multiple of 8, odd T
+from 2048 tiles), causal problems of 320 to 512 groups of 128 queries with at least 4096
+keys (a multiple of 256) in pairs of 128-query tiles whose keys two wave groups split, the
+128-query kernel from 200 (noncausal) or 320 (causal) groups of 128 queries, and otherwise
+the key-split kernel: up to 256 query blocks of 32, 4 waves with 64-key tiles
 (noncausal from 1024 keys with dedicated DMA waves; causal from 512 to 2047 keys, pairs of
 16-query blocks; 8 waves with 32-key tiles from 2048 keys on; 32-key tiles when 64-key
 tiles would split unevenly over the waves, and causal below 512 keys), and 32-key tiles
@@ -42,7 +42,8 @@ CASES = [
     (1, 128, 1024, False, "256-query (512 groups of 256)", K.FA2_KERNEL_256_QUERY),
     (1, 36, 4096, False, "128-query (576 wide workgroups: a partial last round)", K.FA2_KERNEL_128_QUERY),
     (3, 16, 4096, False, "256-query (768 wide workgroups: a half-full last round)", K.FA2_KERNEL_256_QUERY),
-    (1, 31, 1024, False, "key-split, 32-key tiles (248 groups of 128)", K.FA2_KERNEL_KEY_SPLIT_32),
+    (1, 24, 1024, False, "key-split, 32-key tiles (192 groups of 128)", K.FA2_KERNEL_KEY_SPLIT_32),
+    (1, 25, 1024, False, "128-query (200 groups of 128)", K.FA2_KERNEL_128_QUERY),
     (1, 32, 1024, False, "128-query (256 groups of 128)", K.FA2_KERNEL_128_QUERY),
     (1, 8, 1024, False, "key-split, 64-key tiles, DMA waves (256 query blocks)", K.FA2_KERNEL_KEY_SPLIT_64_DMA_WAVES),
     (1, 8, 768, False, "key-split, 64-key tiles (192 blocks, 12 tiles over 4 waves)", K.FA2_KERNEL_KEY_SPLIT_64),
@@ -74,9 +75,13 @@ CASES = [
     (2, 256, 256, False, "256-query (512 groups, the shortest key stream: 4 tiles)", K.FA2_KERNEL_256_QUERY),
     (8, 256, 256, True, "256-query, single tiles (2048 heads of one query tile)", K.FA2_KERNEL_256_QUERY),
     (1, 504, 1024, True, "256-query, tile pairs (2016 tiles of T = 4)", K.FA2_KERNEL_256_QUERY_PAIRS),
-    (32, 16, 1024, True, "256-query, head groups (2048 tiles of T = 4)", K.FA2_KERNEL_256_QUERY),
+    (32, 16, 1024, True, "256-query, tile pairs (2048 tiles of T = 4)", K.FA2_KERNEL_256_QUERY_PAIRS),
+    (8, 16, 2048, True, "256-query, tile pairs (1024 tiles of T = 8)", K.FA2_KERNEL_256_QUERY_PAIRS),
     (1, 64, 4096, True, "256-query, head groups (1024 tiles of T = 16)", K.FA2_KERNEL_256_QUERY),
     (1, 66, 4096, True, "256-query, single tiles (XCD ranges splitting heads)", K.FA2_KERNEL_256_QUERY),
+    (64, 16, 512, True, "256-query, tile pairs (2048 tiles of T = 2)", K.FA2_KERNEL_256_QUERY_PAIRS),
+    (128, 16, 512, True, "256-query, head groups (4096 tiles of T = 2)", K.FA2_KERNEL_256_QUERY),
+    (1, 20, 16384, True, "256-query, tile pairs (20 heads: XCD ranges would split heads)", K.FA2_KERNEL_256_QUERY_PAIRS),
     (1, 8, 8192, True, "128-query tile pairs split over two wave groups (512 groups of 128)",
      K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS),
     (1, 5, 8192, True, "128-query tile pairs split over two wave groups (320 groups, the fewest)",
@@ -84,7 +89,11 @@ CASES = [
     (1, 3, 16384, True, "128-query tile pairs split over two wave groups (16384 keys)",
      K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS),
     (1, 9, 8192, True, "128-query (576 groups of 128, beyond one round)", K.FA2_KERNEL_128_QUERY),
-    (1, 16, 4096, True, "128-query (512 groups of 128, below 8192 keys)", K.FA2_KERNEL_128_QUERY),
+    (1, 16, 4096, True, "128-query tile pairs split over two wave groups (512 groups, 4096 keys)",
+     K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS),
+    (1, 10, 4096, True, "128-query tile pairs split over two wave groups (320 groups of 4096 keys)",
+     K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS),
+    (1, 32, 2048, True, "128-query (512 groups of 128, below 4096 keys)", K.FA2_KERNEL_128_QUERY),
     (1, 5, 8320, True, "128-query (325 groups, an odd number of 128-query tiles per head)", K.FA2_KERNEL_128_QUERY),
 ]
 

@@ -57,7 +57,7 @@ SHAPES = [
     ((1, 8, 768), False, capi.FA2_KERNEL_KEY_SPLIT_64),
     ((1, 9, 1024), False, capi.FA2_KERNEL_KEY_SPLIT_32), ((1, 8, 384), True, capi.FA2_KERNEL_KEY_SPLIT_32),
     ((1, 64, 1024), False, capi.FA2_KERNEL_128_QUERY), ((1, 64, 1024), True, capi.FA2_KERNEL_128_QUERY),
-    ((8, 16, 1024), False, capi.FA2_KERNEL_256_QUERY), ((8, 64, 1024), True, capi.FA2_KERNEL_256_QUERY),
+    ((8, 16, 1024), False, capi.FA2_KERNEL_256_QUERY), ((8, 256, 256), True, capi.FA2_KERNEL_256_QUERY),
     ((8, 64, 512), True, capi.FA2_KERNEL_256_QUERY_PAIRS), ((1, 4, 2048), False, capi.FA2_KERNEL_KEY_SPLIT_8_WAVES),
     ((1, 2, 4096), True, capi.FA2_KERNEL_KEY_SPLIT_8_WAVES),
     ((1, 5, 8192), True, capi.FA2_KERNEL_128_QUERY_SPLIT_PAIRS),

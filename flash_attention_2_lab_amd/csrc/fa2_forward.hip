@@ -2145,8 +2145,10 @@ void fa2_forward_d64_split_pairs_kernel(const _Float16* __restrict__ query,
     // O / l of one 32-query block as FP16: accumulator i of d-block dblk holds dim
     // 32*dblk + 8*(i/4) + 4*half + i%4 of the lane's query. Staged through the wave's
     // output block in LDS (chunk c of row r at c ^ (r & 7)) and read back a row per 8
-    // lanes, so that every store instruction writes whole 128-byte rows. Only this wave
-    // touches its block, and its LDS accesses complete in order: no barrier.
+    // lanes, so that every store instruction writes whole 128-byte rows. Waves w and w+4
+    // share block w: group 1 uses it for the light tile inside the key loop, group 0
+    // after the merge, with workgroup barriers in between; within one use a wave's LDS
+    // accesses complete in order, so no barrier of its own.
     uint8_t* const out_lds = smem + 2 * kRingBytes + gw * kOutBytes;
     auto store_block = [&](const f32x16 (&o)[2], float l_lane, int q_first) {
         const float inv_l = 1.0f / sum_across_halves(l_lane);

@@ -1731,7 +1731,11 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
     constexpr int kStages = 4;
     constexpr int kStageBytes = 2 * kTileBytes;
     constexpr int kDmaPerTile = kStageBytes / 1024 / kWaves;  // LDS-DMA instructions per wave
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages * kStageBytes];
+    // Causal with one query tile per workgroup: the last key tile gets a fifth stage of its
+    // own (fetched with the prologue), so that the four diagonal tiles are in LDS together
+    // and the waves run them without barriers (80 KiB: still two workgroups per CU).
+    constexpr bool kFreeDiag = kCausal && !kPairs;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[(kStages + (kFreeDiag ? 1 : 0)) * kStageBytes];
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1760,9 +1764,10 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
     const uint32_t smem_addr = lds_address(smem);
     const int dma_off[2] = {dma_lane_offset(lane, 0), dma_lane_offset(lane, 1)};
     // This wave issues instructions n = wave + x * kWaves of a tile's 16 (8 per
-    // matrix, 8 rows each).
-    auto dma_tile = [&](int t) {
-        const uint32_t stage = smem_addr + (uint32_t)((t & (kStages - 1)) * kStageBytes);
+    // matrix, 8 rows each), into ring stage t % 4 or the named stage.
+    auto dma_tile = [&](int t, int stage_index = -1) {
+        if (stage_index < 0) stage_index = t & (kStages - 1);
+        const uint32_t stage = smem_addr + (uint32_t)(stage_index * kStageBytes);
 #pragma unroll
         for (int x = 0; x < kDmaPerTile; ++x) {
             const int n = wave + x * kWaves;
@@ -1784,9 +1789,9 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
         k_addr[ks] = smem_addr + (uint32_t)(k_row * kRowBytes + (((2 * ks + half) ^ k_swz) << 4));
         asm volatile("" : "+v"(k_addr[ks]));
     }
-    // K fragments of tile t: kf[key block][16-dim step].
-    auto read_k = [&](int t, f16x8 (&kf)[2][4]) {
-        const uint32_t stage_off = (uint32_t)((t & (kStages - 1)) * kStageBytes);
+    // K fragments of the tile in LDS stage `stage_index`: kf[key block][16-dim step].
+    auto read_k = [&](int stage_index, f16x8 (&kf)[2][4]) {
+        const uint32_t stage_off = (uint32_t)(stage_index * kStageBytes);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const FA2_LDS f16x8* frag = reinterpret_cast<const FA2_LDS f16x8*>((size_t)(k_addr[ks] + stage_off));
@@ -1811,7 +1816,9 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
     // Epilogue of a pass: O = O^T / l. Accumulator i of d-block dblk holds dim
     // 32*dblk + 8*(i/4) + 4*half + i%4 of the lane's query.
     // Staged through this wave's 4 KiB of stage 3 (free after the last tile's barrier; the
-    // next pass's prologue fetches into stages 0..2): chunk c of row r at c ^ (r & 7).
+    // next pass's prologue fetches into stages 0..2; with the fifth stage no diagonal tile is
+    // in stage 3, which is free from the barrier after the last tile before the diagonal):
+    // chunk c of row r at c ^ (r & 7).
     auto store = [&](const f32x16 (&o)[2], float l_run, int q) {
         const float inv_l = 1.0f / sum_across_halves(l_run);
         // The lane index recomputed here, so that nothing but the accumulators stays live
@@ -1868,6 +1875,7 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
         dma_tile(0);
         dma_tile(1);  // num_tiles >= 4: seq_len and the causal key range are multiples of 256
         dma_tile(2);
+        if constexpr (kFreeDiag) dma_tile(num_tiles - 1, kStages);  // the last diagonal tile
 
         f32x16 oa[2], ob[2];
 #pragma unroll
@@ -1891,18 +1899,29 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
         // One key tile: fetch three ahead, and after the work, wait for tile t+1 (only the
         // fetches of the tiles after it may stay in flight) at a barrier, after which
         // every wave is done with tile t's stage.
+        // kFreeDiag: the ring carries tiles 0..num_tiles-2; the barrier after the last tile
+        // before the diagonal (tile num_tiles-5) waits for every fetch, and the four diagonal
+        // tiles pass no barrier: each wave runs its own (both blocks up to block a's diagonal
+        // tile, then block b alone), 5 block-tiles per wave where a barrier per tile made 6.
         auto fetch_ahead = [&](int t) {
-            if (t + 3 < num_tiles) dma_tile(t + 3);  // into the stage tile t-1 used
+            if (t + 3 < num_tiles - (kFreeDiag ? 1 : 0)) dma_tile(t + 3);  // into the stage tile t-1 used
         };
         auto tile_done = [&](int t) {
-            if (t + 3 < num_tiles) wait_dma_and_barrier<2 * kDmaPerTile>();
-            else if (t + 2 < num_tiles) wait_dma_and_barrier<kDmaPerTile>();
-            else wait_dma_and_barrier<0>();
+            if constexpr (kFreeDiag) {
+                if (t + 5 < num_tiles) wait_dma_and_barrier<2 * kDmaPerTile>();
+                else if (t + 5 == num_tiles) wait_dma_and_barrier<0>();
+            } else {
+                if (t + 3 < num_tiles) wait_dma_and_barrier<2 * kDmaPerTile>();
+                else if (t + 2 < num_tiles) wait_dma_and_barrier<kDmaPerTile>();
+                else wait_dma_and_barrier<0>();
+            }
         };
+        auto stage_of = [&](int t) { return kFreeDiag && t == num_tiles - 1 ? kStages : t & (kStages - 1); };
         int t = 0;
         for (; t <= last_a; ++t) {
             fetch_ahead(t);
-            const uint8_t* v_lds = smem + (t & (kStages - 1)) * kStageBytes + kTileBytes;
+            const int stage_index = stage_of(t);
+            const uint8_t* v_lds = smem + stage_index * kStageBytes + kTileBytes;
             // S^T = K Q^T of both blocks; each K fragment feeds two MFMAs. The MFMA
             // phases run at raised wave priority: when both waves of a SIMD can
             // issue, the one with MFMAs goes first and the other's softmax fills the
@@ -1911,7 +1930,7 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
             // compiler from spreading them over the phases).
             __builtin_amdgcn_s_setprio(1);
             f16x8 kf[2][4];
-            read_k(t, kf);
+            read_k(stage_index, kf);
             __builtin_amdgcn_sched_barrier(0);
             f32x16 sa[2], sb[2];
             const f32x16 zero = {};
@@ -1976,10 +1995,11 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
             // (t >= 1 here, so its running max is set).
             for (; t <= last_b; ++t) {
                 fetch_ahead(t);
-                const uint8_t* v_lds = smem + (t & (kStages - 1)) * kStageBytes + kTileBytes;
+                const int stage_index = stage_of(t);
+                const uint8_t* v_lds = smem + stage_index * kStageBytes + kTileBytes;
                 __builtin_amdgcn_s_setprio(1);
                 f16x8 kf[2][4];
-                read_k(t, kf);
+                read_k(stage_index, kf);
                 __builtin_amdgcn_sched_barrier(0);
                 f32x16 sb[2];
                 const f32x16 zero = {};
@@ -2014,8 +2034,9 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
                 __builtin_amdgcn_s_setprio(0);
                 tile_done(t);
             }
-            // The workgroup's remaining tiles: only the fetches and barriers.
-            for (; t < num_tiles; ++t) {
+            // The workgroup's remaining tiles: only the fetches and barriers (none with the
+            // fifth stage: nothing left to fetch, and the diagonal passes no barrier).
+            for (; !kFreeDiag && t < num_tiles; ++t) {
                 fetch_ahead(t);
                 tile_done(t);
             }

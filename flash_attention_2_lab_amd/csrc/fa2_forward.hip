@@ -1731,10 +1731,10 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
     constexpr int kStages = 4;
     constexpr int kStageBytes = 2 * kTileBytes;
     constexpr int kDmaPerTile = kStageBytes / 1024 / kWaves;  // LDS-DMA instructions per wave
-    // Causal with one query tile per workgroup: the last key tile gets a fifth stage of its
-    // own (fetched with the prologue), so that the four diagonal tiles are in LDS together
-    // and the waves run them without barriers (80 KiB: still two workgroups per CU).
-    constexpr bool kFreeDiag = kCausal && !kPairs;
+    // Causal: the last key tile of a pass gets a fifth stage of its own (fetched with the
+    // pass's prologue), so that the four diagonal tiles are in LDS together and the waves
+    // run them without barriers (80 KiB: still two workgroups per CU).
+    constexpr bool kFreeDiag = kCausal;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[(kStages + (kFreeDiag ? 1 : 0)) * kStageBytes];
 
     const int tid = threadIdx.x;
@@ -1864,14 +1864,16 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
         const int last_b = kCausal ? (q_block + kQueriesPerWave * block_b) / kKeysPerTile : num_tiles - 1;
 
         // Q^T fragments of both blocks (B operands of K Q^T). Tiles 0..2 go to stages
-        // 0..2: the previous pass ended with every wave past a barrier after its last
-        // tile, and with no fetch in flight.
+        // 0..2 and the last tile to stage 4: the previous pass has no fetch in flight, and
+        // its waves ran its diagonal tiles without barriers, so every wave first waits here
+        // for the others to be done with them.
         f16x8 qa[4], qb[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             qa[ks] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(q_head, query_a * kRowBytes + 32 * ks + 16 * half, 0, 0));
             qb[ks] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(q_head, query_b * kRowBytes + 32 * ks + 16 * half, 0, 0));
         }
+        if (kPairs && pass > 0) __builtin_amdgcn_s_barrier();
         dma_tile(0);
         dma_tile(1);  // num_tiles >= 4: seq_len and the causal key range are multiples of 256
         dma_tile(2);

@@ -1731,10 +1731,15 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
     constexpr int kStages = 4;
     constexpr int kStageBytes = 2 * kTileBytes;
     constexpr int kDmaPerTile = kStageBytes / 1024 / kWaves;  // LDS-DMA instructions per wave
-    // Causal: the last key tile of a pass gets a fifth stage of its own (fetched with the
-    // pass's prologue), so that the four diagonal tiles are in LDS together and the waves
-    // run them without barriers (80 KiB: still two workgroups per CU).
-    constexpr bool kFreeDiag = kCausal;
+    // Causal tile pairs: the last key tile of a pass gets a fifth stage of its own, so that
+    // the four diagonal tiles are in LDS together and the waves run them without barriers
+    // (80 KiB: still two workgroups per CU). Measured on MI355X (same process, graph replays,
+    // bit-identical outputs): -2.6% to -5% at B16 H16 N1024, B8 H64 N1024 and B16 H16 N2048.
+    // The head groups keep a barrier per tile: there the last tile fetched with the prologue
+    // gained 1% but raised HBM fetch from 1.03x to 1.15x Q+K+V at B16 H16 N4096 (its tile is
+    // fetched apart from the head's other workgroups), and fetched two tiles before the
+    // diagonal it gained nothing (fetch 1.08x).
+    constexpr bool kFreeDiag = kCausal && kPairs;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[(kStages + (kFreeDiag ? 1 : 0)) * kStageBytes];
 
     const int tid = threadIdx.x;
@@ -1864,9 +1869,9 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
         const int last_b = kCausal ? (q_block + kQueriesPerWave * block_b) / kKeysPerTile : num_tiles - 1;
 
         // Q^T fragments of both blocks (B operands of K Q^T). Tiles 0..2 go to stages
-        // 0..2 and the last tile to stage 4: the previous pass has no fetch in flight, and
-        // its waves ran its diagonal tiles without barriers, so every wave first waits here
-        // for the others to be done with them.
+        // 0..2 (and with four key tiles the last to stage 4): the previous pass has no fetch
+        // in flight, and its waves ran its diagonal tiles without barriers, so every wave
+        // first waits here for the others to be done with them.
         f16x8 qa[4], qb[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
@@ -1877,7 +1882,7 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
         dma_tile(0);
         dma_tile(1);  // num_tiles >= 4: seq_len and the causal key range are multiples of 256
         dma_tile(2);
-        if constexpr (kFreeDiag) dma_tile(num_tiles - 1, kStages);  // the last diagonal tile
+        if (kFreeDiag && num_tiles == 4) dma_tile(3, kStages);  // the last diagonal tile
 
         f32x16 oa[2], ob[2];
 #pragma unroll
@@ -1901,16 +1906,21 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
         // One key tile: fetch three ahead, and after the work, wait for tile t+1 (only the
         // fetches of the tiles after it may stay in flight) at a barrier, after which
         // every wave is done with tile t's stage.
-        // kFreeDiag: the ring carries tiles 0..num_tiles-2; the barrier after the last tile
-        // before the diagonal (tile num_tiles-5) waits for every fetch, and the four diagonal
-        // tiles pass no barrier: each wave runs its own (both blocks up to block a's diagonal
-        // tile, then block b alone), 5 block-tiles per wave where a barrier per tile made 6.
+        // kFreeDiag: the ring carries tiles 0..num_tiles-2, and the last tile goes to stage 4
+        // with the fetch two tiles before the diagonal (d = num_tiles - 4), near the other
+        // fetches of the same keys (measured 1-2% faster than with the prologue's fetches at
+        // B16 H16 N1024, B8 H64 N1024 and B16 H16 N2048). The barrier after the last tile
+        // before the diagonal waits for every fetch, and the four diagonal tiles pass no
+        // barrier: each wave runs its own (both blocks up to block a's diagonal tile, then
+        // block b alone), 5 block-tiles per wave where a barrier per tile made 6.
         auto fetch_ahead = [&](int t) {
             if (t + 3 < num_tiles - (kFreeDiag ? 1 : 0)) dma_tile(t + 3);  // into the stage tile t-1 used
+            if (kFreeDiag && t + 6 == num_tiles) dma_tile(num_tiles - 1, kStages);
         };
         auto tile_done = [&](int t) {
             if constexpr (kFreeDiag) {
-                if (t + 5 < num_tiles) wait_dma_and_barrier<2 * kDmaPerTile>();
+                if (t + 6 < num_tiles) wait_dma_and_barrier<2 * kDmaPerTile>();
+                else if (t + 6 == num_tiles) wait_dma_and_barrier<3 * kDmaPerTile>();  // d, d+1, d+3 in flight
                 else if (t + 5 == num_tiles) wait_dma_and_barrier<0>();
             } else {
                 if (t + 3 < num_tiles) wait_dma_and_barrier<2 * kDmaPerTile>();

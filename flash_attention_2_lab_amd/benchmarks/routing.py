@@ -61,7 +61,7 @@ CASES = (
     Case("head groups vs pairs, causal: T = 16 (throughput shape)", 16, 16, 4096, True, (K.FA2_KERNEL_256_QUERY, K.FA2_KERNEL_256_QUERY_PAIRS)),
     Case("head groups vs pairs, causal: T = 64", 2, 32, 16384, True, (K.FA2_KERNEL_256_QUERY, K.FA2_KERNEL_256_QUERY_PAIRS)),
     Case("pairs vs head groups, causal: T = 2, 2048 tiles", 64, 16, 512, True, (K.FA2_KERNEL_256_QUERY, K.FA2_KERNEL_256_QUERY_PAIRS)),
-    Case("head groups vs pairs, causal: T = 2, 4096 tiles", 128, 16, 512, True, (K.FA2_KERNEL_256_QUERY, K.FA2_KERNEL_256_QUERY_PAIRS)),
+    Case("pairs vs head groups, causal: T = 2, 4096 tiles", 128, 16, 512, True, (K.FA2_KERNEL_256_QUERY, K.FA2_KERNEL_256_QUERY_PAIRS)),
     Case("128-query vs split pairs, causal: 2048 keys", 1, 32, 2048, True, (K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS, K.FA2_KERNEL_128_QUERY)),
     Case("split pairs vs 128-query, causal: 4096 keys, 320 groups", 1, 10, 4096, True, (K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS, K.FA2_KERNEL_128_QUERY)),
     Case("split pairs vs 128-query, causal: 4096 keys, 512 groups", 1, 16, 4096, True, (K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS, K.FA2_KERNEL_128_QUERY)),

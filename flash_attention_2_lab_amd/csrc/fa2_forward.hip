@@ -2406,19 +2406,16 @@ hipError_t launch_split_pairs(const void* q, const void* k, const void* v, void*
                                                              q, k, v, o, (int)seq_len, (int)query_tiles, scale_log2);
 }
 
-// Causal 256-query problems with T = 4 or 8 query tiles per head, or T = 2 below 4096
-// tiles, run pairs of tiles (T-1-p, then p) per workgroup, which give every workgroup
-// the same work; otherwise (T odd, T >= 16, or T = 2 from 4096 tiles) one query tile
-// per workgroup in the level order of xcd_work_item (per-XCD head groups), whose
-// workgroups share each head's K/V through one L2 (HBM fetch 1.05x Q+K+V at B16 H16
-// N4096 against 1.8x for pairs). Re-measured on MI355X with the K and V^T reads issued
-// ahead of their phases (same process, graph replays, head groups -> pairs): -7% to -8%
-// at T = 4 (B32 H16 N1024, B8 H64 N1024), -6% at T = 8 with 1024 tiles (B8 H16 N2048),
-// -1.4% to -3% at T = 8 (B16 H16 N2048, B4 H64 N2048, B16 H32 N2048, B32 H16 N2048);
-// at T = 16 to 64 within 0 to -2% (B16 H16 N4096: 0; B4 H16 N4096, B1 H64 N4096, B2 H16
-// N8192, B2 H32 N16384), where the groups' lower traffic is kept; at T = 2, -3.7% at
-// 2048 tiles (B64 H16 N512) but +2.6% at 4096 (B128 H16 N512). Before that schedule
-// change the head groups measured 1-6% faster than pairs from T = 8 or 2048 tiles on.
+// Causal 256-query problems with T = 2, 4 or 8 query tiles per head run pairs of tiles
+// (T-1-p, then p) per workgroup, which give every workgroup the same work; otherwise (T odd
+// or T >= 16) one query tile per workgroup in the level order of xcd_work_item (per-XCD
+// head groups), whose workgroups share each head's K/V through one L2 (HBM fetch 1.03-1.09x
+// Q+K+V at B16 H16 N4096 against 1.8x for pairs). Measured on MI355X with the pairs' diagonal
+// tiles run without barriers (same process, graph replays, head groups -> pairs): -13% at
+// T = 4 (B16 H16 N1024), -9% (B32 H16 N1024), -4.5% at T = 8 (B8 H16 N2048); at T = 2 -3.6% to
+// -5.5% from 2048 to 8192 tiles (B64 to B512 H16 N512, B64 H64 N512, B128 H32 N512); at T = 16
+// and 32 -0.6% to -1.7% (B16 H16 N4096, B8 H32 N4096, B32 H16 N4096, B4 and B8 H16 N8192) and
+// -1.1% at T = 64 (B2 H32 N16384), where the groups' lower traffic is kept.
 // When batch*heads is not a multiple of 8 the XCD ranges split heads, and an XCD whose
 // range holds a split head's heavy tiles gets more work: up to 8/batch_heads of a head's
 // share more (5.5% at 36 heads; 82% for one head), so single tiles need 32 heads or more
@@ -2426,8 +2423,7 @@ hipError_t launch_split_pairs(const void* q, const void* k, const void* v, void*
 bool use_head_groups(int64_t batch_heads, int64_t tiles_per_head) {
     if (tiles_per_head % 2 != 0) return true;
     if (batch_heads % 8 != 0 && batch_heads < 32) return false;
-    if (tiles_per_head >= 16) return true;
-    return tiles_per_head == 2 && batch_heads * tiles_per_head >= 4096;
+    return tiles_per_head >= 16;
 }
 
 // 256-query workgroups (64 queries per wave) once the grid fills every workgroup

@@ -62,7 +62,7 @@ K = capi
     (7, 16, 2048, False, K.FA2_KERNEL_256_QUERY), (6, 16, 4096, False, K.FA2_KERNEL_256_QUERY),
     # Causal: 256-query from 512 workgroups of tile pairs when a head has an even
     # number T of tiles, single tiles from 2048 with an odd number. Single tiles in
-    # level order at T >= 16 (and T = 2 from 4096 tiles); pairs at T = 4 and 8.
+    # level order at T >= 16; pairs at T = 2, 4 and 8.
     (16, 16, 4096, True, K.FA2_KERNEL_256_QUERY), (1, 256, 1024, True, K.FA2_KERNEL_256_QUERY_PAIRS),
     (1, 255, 1024, True, K.FA2_KERNEL_128_QUERY), (2, 32, 16384, True, K.FA2_KERNEL_256_QUERY),
     (32, 16, 1024, True, K.FA2_KERNEL_256_QUERY_PAIRS), (1, 504, 1024, True, K.FA2_KERNEL_256_QUERY_PAIRS),
@@ -97,10 +97,10 @@ K = capi
     # Sequence lengths the production entry rejects but the Bc16/Bc32 entries take
     # (partial last block) run the key-split kernel.
     (4, 64, 1040, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 2, 80, False, K.FA2_KERNEL_KEY_SPLIT_32), (1, 2, 240, False, K.FA2_KERNEL_KEY_SPLIT_64),
-    # Causal 256-query: pairs of tiles at T = 4 and 8 (T = 2 below 4096 tiles), head groups
+    # Causal 256-query: pairs of tiles at T = 2, 4 and 8, head groups
     # at T >= 16 or odd; split pairs from 4096 keys at 320-512 groups of 128.
     (32, 16, 1024, True, K.FA2_KERNEL_256_QUERY_PAIRS), (8, 16, 2048, True, K.FA2_KERNEL_256_QUERY_PAIRS),
-    (16, 16, 4096, True, K.FA2_KERNEL_256_QUERY), (128, 16, 512, True, K.FA2_KERNEL_256_QUERY),
+    (16, 16, 4096, True, K.FA2_KERNEL_256_QUERY), (128, 16, 512, True, K.FA2_KERNEL_256_QUERY_PAIRS),
     (64, 16, 512, True, K.FA2_KERNEL_256_QUERY_PAIRS), (1, 20, 16384, True, K.FA2_KERNEL_256_QUERY_PAIRS),
     (1, 16, 4096, True, K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS), (1, 32, 2048, True, K.FA2_KERNEL_128_QUERY),
     # Nothing to launch.

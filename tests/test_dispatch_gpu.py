@@ -3,8 +3,8 @@
 The forward picks its kernel from (batch*heads, seq_len, causal) (fa2_forward.hip,
 `choose_kernel`): the 256-query kernel from 512 workgroups (noncausal: unless its grid
 ends in a partial round that the 128-query kernel's finer rounds finish sooner; causal:
-pairs of query tiles at T = 4 and 8 tiles per head, at T = 2 below 4096 tiles, and at any
-even T when batch*heads is below 32 and not a multiple of 8; otherwise one query tile per
+pairs of query tiles at T = 2, 4 and 8 tiles per head, and at any even T when batch*heads
+is below 32 and not a multiple of 8; otherwise one query tile per
 workgroup in level order, per-XCD head groups when batch*heads is a multiple of 8, odd T
 from 2048 tiles), causal problems of 320 to 512 groups of 128 queries with at least 4096
 keys (a multiple of 256) in pairs of 128-query tiles whose keys two wave groups split, the
@@ -80,7 +80,7 @@ CASES = [
     (1, 64, 4096, True, "256-query, head groups (1024 tiles of T = 16)", K.FA2_KERNEL_256_QUERY),
     (1, 66, 4096, True, "256-query, single tiles (XCD ranges splitting heads)", K.FA2_KERNEL_256_QUERY),
     (64, 16, 512, True, "256-query, tile pairs (2048 tiles of T = 2)", K.FA2_KERNEL_256_QUERY_PAIRS),
-    (128, 16, 512, True, "256-query, head groups (4096 tiles of T = 2)", K.FA2_KERNEL_256_QUERY),
+    (128, 16, 512, True, "256-query, tile pairs (4096 tiles of T = 2)", K.FA2_KERNEL_256_QUERY_PAIRS),
     (1, 20, 16384, True, "256-query, tile pairs (20 heads: XCD ranges would split heads)", K.FA2_KERNEL_256_QUERY_PAIRS),
     (1, 8, 8192, True, "128-query tile pairs split over two wave groups (512 groups of 128)",
      K.FA2_KERNEL_128_QUERY_SPLIT_PAIRS),

@@ -1908,7 +1908,7 @@ void fa2_forward_d64_wide_kernel(const _Float16* __restrict__ query,
         // every wave is done with tile t's stage.
         // kFreeDiag: the ring carries tiles 0..num_tiles-2, and the last tile goes to stage 4
         // with the fetch two tiles before the diagonal (d = num_tiles - 4), near the other
-        // fetches of the same keys (measured 1-2% faster than with the prologue's fetches at
+        // fetches of the same keys (measured 1-3% faster than with the prologue's fetches at
         // B16 H16 N1024, B8 H64 N1024 and B16 H16 N2048). The barrier after the last tile
         // before the diagonal waits for every fetch, and the four diagonal tiles pass no
         // barrier: each wave runs its own (both blocks up to block a's diagonal tile, then

@@ -453,7 +453,7 @@ def test_concurrent_streams_do_not_interfere():
     # The forward keeps no state between calls (no scratch memory, no counters), so
     # calls on different streams may overlap. Three side streams each run ten forwards
     # of their own shape and inputs (256-query kernel, causal pairs; key-split kernel;
-    # causal split pairs, 128 KiB of LDS per workgroup) at the same time; every output
+    # causal split pairs, 144 KiB of LDS per workgroup) at the same time; every output
     # must equal the sequential result bitwise.
     cases = [((8, 64, 1024), True, 51), ((1, 8, 1024), False, 52), ((1, 5, 8192), True, 53)]
     inputs = [[t.cuda() for t in _inputs(*shape, seed=seed)] for shape, _, seed in cases]
